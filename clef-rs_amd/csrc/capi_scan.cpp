@@ -1,0 +1,96 @@
+// C ABI: error plumbing and the gated-DeltaNet scan entry points.
+// Validation happens here, before any launch (metal.rs:280-290, 303-307).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <string>
+
+#include "../../include/clef_hip.h"
+#include "common.hpp"
+#include "scan.hpp"
+
+namespace clef {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(static_cast<int>(e), std::string(what) + ": " + hipGetErrorString(e));
+  return 0;
+}
+
+}  // namespace clef
+
+using clef::fail;
+
+extern "C" const char* clef_hip_last_error(void) { return clef::g_last_error.c_str(); }
+
+extern "C" int clef_hip_abi_version(void) { return 1; }
+
+static bool valid_dtype(int d) { return d == CLEF_F32 || d == CLEF_F16; }
+
+static int scan_dims(int T, int Hk, int Hv, int dk, int dv, int chunk, int precision) {
+  CLEF_REQUIRE(T >= 1 && T <= (1 << 20), "DeltaNet scan: tokens must be in 1..1048576");
+  CLEF_REQUIRE(Hk >= 1 && Hv >= Hk && Hv <= 256 && Hv % Hk == 0,
+               "DeltaNet scan: heads must satisfy 1 <= Hk <= Hv <= 256, Hv % Hk == 0");
+  CLEF_REQUIRE(dk >= 1 && dk <= 128 && dv >= 1 && dv <= 128,
+               "DeltaNet scan: key and value widths must be in 1..128");
+  CLEF_REQUIRE(chunk == 64, "DeltaNet scan: chunk must be 64");
+  CLEF_REQUIRE(precision == CLEF_SCAN_STRICT || precision == CLEF_SCAN_MIXED,
+               "DeltaNet scan: unknown precision profile");
+  return 0;
+}
+
+extern "C" size_t clef_delta_scan_workspace(int T, int Hk, int Hv, int dk, int dv, int chunk,
+                                            int precision) {
+  if (scan_dims(T, Hk, Hv, dk, dv, chunk, precision)) return 0;
+  return clef::scan_workspace_bytes(T, Hk, Hv, precision);
+}
+
+extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk,
+                               int64_t sv, int dtype_qkv, const void* g, const void* beta,
+                               int64_t sgb, int dtype_gb, int T, int Hk, int Hv, int dk, int dv,
+                               int chunk, int precision, const float* initial, int capture,
+                               void* out, int64_t so, int dtype_out, float* captured,
+                               float* final_state, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (int rc = scan_dims(T, Hk, Hv, dk, dv, chunk, precision)) return rc;
+  CLEF_REQUIRE(q && k && v && g && beta && out, "DeltaNet scan: null input or output");
+  CLEF_REQUIRE(valid_dtype(dtype_qkv) && valid_dtype(dtype_gb) && valid_dtype(dtype_out),
+               "DeltaNet scan: unsupported dtype");
+  if (sqk == 0) sqk = static_cast<int64_t>(Hk) * dk;
+  if (sv == 0) sv = static_cast<int64_t>(Hv) * dv;
+  if (sgb == 0) sgb = Hv;
+  if (so == 0) so = static_cast<int64_t>(Hv) * dv;
+  CLEF_REQUIRE(sqk >= static_cast<int64_t>(Hk) * dk && sv >= static_cast<int64_t>(Hv) * dv &&
+                   sgb >= Hv && so >= static_cast<int64_t>(Hv) * dv,
+               "DeltaNet scan: token stride smaller than a token row");
+  CLEF_REQUIRE(capture >= 0 && capture <= T, "DeltaNet scan: capture must be in 0..T");
+  CLEF_REQUIRE(capture == 0 || captured, "DeltaNet scan: capture requested without a buffer");
+  const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, precision);
+  CLEF_REQUIRE(workspace && workspace_bytes >= need, "DeltaNet scan: workspace too small");
+  CLEF_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+               "DeltaNet scan: workspace must be 256-byte aligned");
+
+  clef::ScanParams p{};
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta;
+  p.sqk = sqk; p.sv = sv; p.sgb = sgb; p.so = so;
+  p.dtype_qkv = dtype_qkv; p.dtype_gb = dtype_gb; p.dtype_out = dtype_out;
+  p.T = T; p.Hk = Hk; p.Hv = Hv; p.dk = dk; p.dv = dv;
+  p.nchunks = (T + 63) / 64;
+  const int vi = dtype_qkv == CLEF_F32 ? 4 : 8;
+  p.vec_qk = (dk % vi == 0) && (sqk % vi == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0) &&
+             ((reinterpret_cast<uintptr_t>(k) & 15) == 0);
+  p.qscale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dk)));
+  p.initial = initial; p.capture = capture;
+  p.out = out; p.captured = captured; p.final_state = final_state;
+  clef::scan_carve_workspace(p, workspace, precision);
+  return clef::scan_launch(p, precision, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 kernels: element conversion, MFMA
+// fragments, error plumbing.  Wavefronts are 64 lanes.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+namespace clef {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+// ---- scalar conversions --------------------------------------------------
+template <class T> __device__ __forceinline__ float to_f32(T x) { return static_cast<float>(x); }
+template <class T> __device__ __forceinline__ T from_f32(float x) { return static_cast<T>(x); }
+
+// ---- MFMA fragments ------------------------------------------------------
+// A fragment is 16 bytes per lane covering one "k-block" of a 16x16 tile:
+//   f16: 8 halves, k-block of 32, one v_mfma_f32_16x16x32_f16;
+//   f32: 4 floats, k-block of 16, four v_mfma_f32_16x16x4_f32.
+// Operands are stored K-contiguous ([rows][K]).  Lane l supplies row l%16
+// and the 16 bytes at byte offset 16*(l/16) of the k-block, for both A and B
+// (B given as [N][K]); for f32 the four floats of a lane feed four MFMAs
+// whose k index is 4*(l/16)+s, a permutation of k applied to both operands.
+// The accumulator layout is that of the hardware: lane l holds rows
+// 4*(l/16)+i (i = 0..3) of column l%16.
+template <class T> struct Mma;
+
+template <> struct Mma<half_t> {
+  typedef half8 frag;
+  static constexpr int kBlock = 32;
+  static __device__ __forceinline__ void mma(float4_t& c, const frag& a, const frag& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mma<float> {
+  typedef float4_t frag;
+  static constexpr int kBlock = 16;
+  static __device__ __forceinline__ void mma(float4_t& c, const frag& a, const frag& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
+  }
+};
+
+template <class T>
+__device__ __forceinline__ typename Mma<T>::frag load_frag(const T* p) {
+  return *reinterpret_cast<const typename Mma<T>::frag*>(p);
+}
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---- host-side error plumbing ---------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);  // records msg, returns code
+int check_launch(const char* what);          // hipGetLastError -> 0 or >0
+
+}  // namespace clef
+
+#define CLEF_REQUIRE(cond, msg)                              \
+  do {                                                       \
+    if (!(cond)) return ::clef::fail(-1, std::string(msg));  \
+  } while (0)

@@ -1,0 +1,178 @@
+/*
+ * clef_hip.h -- C ABI of the MI355X (gfx950) hybrid-backbone prefill path.
+ *
+ * Each entry point replaces one device custom op of clef-rs's Metal backend
+ * (paths relative to the clef-rs repository root) and keeps its semantics:
+ * the same shapes, the same op contract, validation before any launch.
+ *
+ * Conventions
+ *  - Buffers are device pointers owned by the caller; the library allocates
+ *    no persistent memory.  Scratch space is passed in as `workspace`.
+ *  - Every call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ *    stream) and never synchronizes the host.
+ *  - Return value: 0 on success; < 0 validation error (nothing was launched);
+ *    > 0 a HIP error code from the launch.  clef_hip_last_error() returns the
+ *    message of the calling thread's last failure.
+ *  - Tensors are row-major.  "Token stride" arguments give the distance in
+ *    elements between consecutive tokens (rows) so that views into a packed
+ *    projection output can be passed without a copy; 0 means contiguous.
+ *  - dtype codes: CLEF_F32 = 0, CLEF_F16 = 1 (IEEE binary16).
+ */
+#ifndef CLEF_HIP_H
+#define CLEF_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { CLEF_F32 = 0, CLEF_F16 = 1 };
+/* Scan arithmetic profile.  STRICT: f32 operands on f32 MFMA (parity with the
+ * CPU F32 path at rtol 1e-4 / atol 1e-5).  MIXED: f16 operands on f16 MFMA
+ * with f32 accumulation and an f32 state (rtol 2e-2). */
+enum { CLEF_SCAN_STRICT = 0, CLEF_SCAN_MIXED = 1 };
+
+const char* clef_hip_last_error(void);
+int clef_hip_abi_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* Gated DeltaNet scan                                                     */
+/* ---------------------------------------------------------------------- */
+/*
+ * Replaces DeltaKernel::{forward, prepared_prefill, prefill} and the
+ * "clef-fused-delta" / "clef-cached-delta" custom ops
+ * (crates/core/src/models/metal.rs:161-278, 291-413), whose CPU definition is
+ * delta_recurrence_prefill (crates/core/src/models/qwen.rs:826-882):
+ *   q <- l2(q)/sqrt(dk), k <- l2(k), l2(x) = x/sqrt(sum x^2 + 1e-6)
+ *   per token: S <- S*exp(g); d = (v - S^T k)*beta; S <- S + k d^T; o = S^T q
+ * with v-head i reading k-head i/(Hv/Hk) (repeat-interleave, qwen.rs:727-738).
+ *
+ * q, k: [T, Hk, dk] (token strides sqk, dtype_qkv); v: [T, Hv, dv] (token
+ * stride sv, dtype_qkv); g (log-decay), beta: [T, Hv] (token stride sgb,
+ * dtype_gb).  out: [T, Hv, dv] (token stride so, dtype_out).
+ * initial: [Hv, dk, dv] f32 or NULL (zero state).  capture in 1..T writes the
+ * state after token `capture` to captured [Hv, dk, dv]; 0 = none.
+ * final_state [Hv, dk, dv] f32 or NULL receives the state after token T.
+ * Limits: 1 <= T <= 1048576; 1 <= Hk <= Hv <= 256; Hv % Hk == 0;
+ * 1 <= dk <= 128; 1 <= dv <= 128; chunk == 64.
+ */
+size_t clef_delta_scan_workspace(int T, int Hk, int Hv, int dk, int dv, int chunk, int precision);
+int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
+                    int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
+                    int T, int Hk, int Hv, int dk, int dv, int chunk, int precision,
+                    const float* initial, int capture, void* out, int64_t so, int dtype_out,
+                    float* captured, float* final_state, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Projections                                                             */
+/* ---------------------------------------------------------------------- */
+/*
+ * y[M,N] = x[M,K] . W[N,K]^T  (W row-major [N,K], the checkpoint layout).
+ * Replaces GemmKernel::forward / "clef-metal4-gemm" (neural.rs:50-55,
+ * 151-173; neural.metal:72-97) and candle_nn::Linear (projection.rs:82-95).
+ * dtype_in CLEF_F16: f16 operands on f16 MFMA, f32 accumulation;
+ * CLEF_F32: f32 operands on f32 MFMA.  x and W share dtype_in.
+ * epilogue: CLEF_EPI_STORE writes y in dtype_out (f16 output is rounded once
+ * from the f32 accumulator, as neural.metal:23-26);
+ * CLEF_EPI_RESIDUAL adds the (dtype_out-rounded) product into an f32 residual
+ * y (h += to_f32(round(x W^T)), qwen.rs:399-410).
+ * Leading dimensions ldx, ldw, ldy in elements (0 = K, K, N).
+ */
+enum { CLEF_EPI_STORE = 0, CLEF_EPI_RESIDUAL = 1 };
+int clef_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+              int M, int N, int K, int dtype_in, int dtype_out, int epilogue, void* stream);
+/*
+ * y[M,N] = silu(x Wg^T) * (x Wu^T).  Replaces GemmKernel::gated /
+ * "clef-metal4-gated" (neural.rs:56-58; neural.metal:29-44, 99-125) and
+ * Projection::gated_forward (projection.rs:67-81).  In f16 the gate, its silu,
+ * the up product and the result are each rounded to half, as the reference
+ * kernel does.
+ */
+int clef_gemm_swiglu(const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
+                     void* y, int64_t ldy, int M, int N, int K, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Pointwise pieces around the scan                                        */
+/* ---------------------------------------------------------------------- */
+/*
+ * RMSNorm y = (x * 1/sqrt(mean(x^2)+eps)) * w, rows of `width`.
+ * Replaces Rms::forward / "clef-rms" (normalization.rs:62-74; ops.rs:17-32;
+ * pointwise.metal:7-43).  w is f32 and already includes any (1+w) offset.
+ * x token stride ldx, y token stride ldy (0 = width).
+ */
+int clef_rms_norm(const void* x, int64_t ldx, int dtype_in, const float* w, void* y, int64_t ldy,
+                  int dtype_out, int rows, int width, float eps, void* stream);
+/*
+ * Depthwise causal conv (taps oldest->newest, zero padded) followed by SiLU,
+ * over `history_rows` cached rows followed by T new rows.  Replaces
+ * causal_convolution + silu (qwen.rs:609-618, 765-796) and "clef-conv"
+ * (pointwise.metal:46-65).  x: [T, W] (stride ldx, dtype_in); history:
+ * [history_rows, W] f32 or NULL; w: [W, taps] f32; y: [T, W] (stride ldy,
+ * dtype_out).  taps <= 8, history_rows <= taps - 1.
+ */
+int clef_conv_silu(const void* x, int64_t ldx, int dtype_in, const float* history,
+                   int history_rows, const float* w, int taps, void* y, int64_t ldy, int dtype_out,
+                   int T, int W, void* stream);
+/*
+ * Decay and write strength from the a/b projections (qwen.rs:619-627):
+ * g = softplus(a + dt) * -exp(A_log) (stable softplus), beta = sigmoid(b).
+ * a, b: [T, Hv] (token strides lda, ldb, dtype_in); dt, a_log: [Hv] f32;
+ * g, beta: [T, Hv] f32 contiguous.
+ */
+int clef_delta_gates(const void* a, int64_t lda, const void* b, int64_t ldb, int dtype_in,
+                     const float* dt, const float* a_log, float* g, float* beta, int T, int Hv,
+                     void* stream);
+/*
+ * Gated output norm: y = round(rms_w(o)) * silu(z), rows of `width` (one row
+ * per token and v-head), qwen.rs:671-676.  o: [rows, width] f32; z: (stride
+ * ldz per token row of Hv*width, dtype_z); y [rows, width] dtype_out.
+ * `round_dtype` is the dtype the reference casts the norm output to first.
+ */
+int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, int dtype_z, const float* w,
+                        void* y, int dtype_out, int T, int Hv, int width, float eps,
+                        void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Gated full-attention layer pieces (qwen.rs:451-525; ops.rs:62-188)      */
+/* ---------------------------------------------------------------------- */
+/*
+ * Per-head RMSNorm (offset weights, eps) then rotary (rotate-half, angle
+ * (pos0 + t) * theta^(-2i/rot_dim) on the first rot_dim features), writing
+ * head-major [H, T_total, d] at token offset `dst_offset` (so cached prefix
+ * keys may precede it).  x: token stride ldx, head stride d.
+ */
+int clef_qk_norm_rotary(const void* x, int64_t ldx, int dtype_in, const float* w, void* y,
+                        int dtype_out, int T, int heads, int d, int rot_dim, double theta,
+                        int pos0, int dst_offset, int dst_tokens, float eps, void* stream);
+/* Head-major copy of values: x [T, heads, d] (token stride ldx) -> y [heads, dst_tokens, d]. */
+int clef_head_major(const void* x, int64_t ldx, int dtype_in, void* y, int dtype_out, int T,
+                    int heads, int d, int dst_offset, int dst_tokens, void* stream);
+/*
+ * Causal GQA attention with online softmax (bottom-right aligned mask when
+ * kn > qn), output gated by sigmoid(gate):
+ *   y[t, h*d + e] = attn(q,k,v)[h, t, e] * sigmoid(gate[t, h*d + e]).
+ * Replaces ops::attention + the sigmoid gate (qwen.rs:511-524) and the
+ * "clef-f32-flash-attention" op (metal.rs:528-633).  q [H, qn, d];
+ * k, v [KVH, kn, d]; gate token stride ldg.  dtype: operand dtype of q/k/v
+ * (f16: f16 MFMA, f32: f32 MFMA), accumulation f32.  d in {64, 128, 256}.
+ */
+int clef_attention_gated(const void* q, const void* k, const void* v, int dtype, int heads,
+                         int kv_heads, int qn, int kn, int d, const void* gate, int64_t ldg,
+                         void* y, int64_t ldy, int dtype_out, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Embedding gather and pooled head                                         */
+/* ---------------------------------------------------------------------- */
+/* h[t, :] = f32(table[ids[t], :]); ids are int32 and must be < vocab. */
+int clef_embed(const int32_t* ids, int T, const void* table, int dtype, int vocab, int H, float* h,
+               void* stream);
+/* logits[j] = sum_k x[row, k] * W[j, k], f32 (last-token pooled head). */
+int clef_head_logits(const float* x, int H, const float* w, int n_logits, float* logits,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
