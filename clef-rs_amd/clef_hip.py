@@ -167,3 +167,45 @@ class DeltaScan:
             T, Hk, Hv, dk, dv, self.chunk, self.precision, _ptr(initial), int(capture),
             _ptr(out), so, _dt(out), _ptr(captured), _ptr(final), _ptr(ws), ws.numel(), _stream()))
         return out, captured, final
+
+
+def _rows(t, name):
+    if t.dim() != 2 or t.stride(1) != 1 or not t.is_cuda:
+        raise ClefError(-1, f"{name} must be a row-major 2-D device tensor")
+    return t.stride(0)
+
+
+def gemm(x, w, out=None, out_dtype=None, residual=None):
+    """y = x . w^T (GemmKernel::forward, neural.rs:50-55).
+
+    x [M,K], w [N,K] share a dtype (f16: f16 MFMA; f32: f32 MFMA), f32
+    accumulation.  With `residual` (an f32 [M,N] tensor) the rounded product
+    is added into it in place and `residual` is returned.
+    """
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or w.dtype != x.dtype:
+        raise ClefError(-1, "GEMM operand shapes or dtypes")
+    out_dtype = out_dtype or x.dtype
+    if residual is not None:
+        if residual.dtype != torch.float32 or residual.shape != (M, N):
+            raise ClefError(-1, "residual must be f32 [M, N]")
+        y, epi, dto = residual, EPI_RESIDUAL, _DT[out_dtype]
+    else:
+        y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x.device)
+        epi, dto = EPI_STORE, _dt(y)
+    _check(lib().clef_gemm(_ptr(x), _rows(x, "x"), _ptr(w), _rows(w, "w"), _ptr(y), _rows(y, "y"),
+                           M, N, K, _dt(x), dto, epi, _stream()))
+    return y
+
+
+def gemm_swiglu(x, wg, wu, out=None):
+    """silu(x wg^T) * (x wu^T) (GemmKernel::gated, neural.rs:56-58)."""
+    M, K = x.shape
+    N = wg.shape[0]
+    if wg.shape != (N, K) or wu.shape != (N, K) or wg.stride(0) != wu.stride(0):
+        raise ClefError(-1, "gated projection weight dimensions")
+    y = out if out is not None else torch.empty((M, N), dtype=x.dtype, device=x.device)
+    _check(lib().clef_gemm_swiglu(_ptr(x), _rows(x, "x"), _ptr(wg), _ptr(wu), _rows(wg, "wg"),
+                                  _ptr(y), _rows(y, "y"), M, N, K, _dt(x), _stream()))
+    return y

@@ -63,6 +63,13 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// Work-group barrier for LDS producer/consumer hand-offs only.  Unlike
+// __syncthreads() it does not wait for outstanding global loads, so register
+// prefetches issued before it stay in flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 

@@ -41,10 +41,6 @@ template <class T> struct Vec16;  // 16-byte vector of T
 template <> struct Vec16<float> { typedef float4_t type; static constexpr int n = 4; };
 template <> struct Vec16<half_t> { typedef half8 type; static constexpr int n = 8; };
 
-__device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype) {
-  return dtype == 0 ? static_cast<const float*>(p)[i] : static_cast<float>(static_cast<const half_t*>(p)[i]);
-}
-
 __device__ __forceinline__ void store_scalar(void* p, int64_t i, int dtype, float v) {
   if (dtype == 0)
     static_cast<float*>(p)[i] = v;
@@ -52,20 +48,34 @@ __device__ __forceinline__ void store_scalar(void* p, int64_t i, int dtype, floa
     static_cast<half_t*>(p)[i] = static_cast<half_t>(v);
 }
 
-// Loads VI consecutive elements (e0.. e0+VI-1) of a row into f32, zero beyond dk.
+// Branch-free row loader: fetches the VI elements e0..e0+VI-1 of a row
+// (clamped into the row so every address is valid) in the input dtype.
+// Conversion and masking happen at use, so the loads stay in flight.
 template <class IT>
-__device__ __forceinline__ void load_row_vec(const IT* row, int e0, int dk, bool vec_ok,
-                                             float (&out)[Vec16<IT>::n]) {
+__device__ __forceinline__ typename Vec16<IT>::type load_row_raw(const IT* row, int e0, int dk,
+                                                                bool vec_ok) {
   constexpr int VI = Vec16<IT>::n;
-  if (vec_ok && e0 + VI <= dk) {
-    typename Vec16<IT>::type v = *reinterpret_cast<const typename Vec16<IT>::type*>(row + e0);
-#pragma unroll
-    for (int i = 0; i < VI; ++i) out[i] = static_cast<float>(v[i]);
+  typename Vec16<IT>::type v;
+  if (vec_ok) {  // dk % VI == 0 and 16-byte aligned rows
+    v = *reinterpret_cast<const typename Vec16<IT>::type*>(row + min(e0, dk - VI));
   } else {
 #pragma unroll
-    for (int i = 0; i < VI; ++i) out[i] = (e0 + i < dk) ? static_cast<float>(row[e0 + i]) : 0.0f;
+    for (int i = 0; i < VI; ++i) v[i] = row[min(e0 + i, dk - 1)];
   }
+  return v;
 }
+
+__device__ __forceinline__ uint32_t load_bits(const void* p, int64_t i, int dtype) {
+  return dtype == 0 ? static_cast<const uint32_t*>(p)[i] : static_cast<const uint16_t*>(p)[i];
+}
+
+__device__ __forceinline__ float bits_to_f32(uint32_t b, int dtype) {
+  if (dtype == 0) return __uint_as_float(b);
+  const uint16_t h = static_cast<uint16_t>(b);
+  return static_cast<float>(*reinterpret_cast<const half_t*>(&h));
+}
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ---------------------------------------------------------------------------
 // Kernel 1: per (chunk, k-head) preparation.
@@ -88,27 +98,35 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   __shared__ float sBeta[2][kC];
 
   const int chunk = blockIdx.x, hk = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int t0 = chunk * kC;
   const int n = min(kC, p.T - t0);
   const int dk = p.dk;
   const float qscale = p.qscale;
 
-  // 1. normalise q and k rows into LDS; record the row scales.
+  // 1. normalise q and k rows into LDS; record the row scales.  All loads
+  //    are issued first (clamped, unconditional), then consumed.
+  constexpr int NPASS = (2 * kC) / RPP;
   const IT* qbase = static_cast<const IT*>(p.q);
   const IT* kbase = static_cast<const IT*>(p.k);
-  for (int rr = tid / TPR; rr < 2 * kC; rr += RPP) {
+  typename Vec16<IT>::type raw[NPASS];
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int rr = ps * RPP + tid / TPR;
+    const bool isq = rr >= kC;
+    const int r = isq ? rr - kC : rr;
+    const IT* row = (isq ? qbase : kbase) + (int64_t)(t0 + min(r, n - 1)) * p.sqk + (int64_t)hk * dk;
+    raw[ps] = load_row_raw<IT>(row, (tid % TPR) * VI, dk, p.vec_qk);
+  }
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int rr = ps * RPP + tid / TPR;
     const bool isq = rr >= kC;
     const int r = isq ? rr - kC : rr;
     const int e0 = (tid % TPR) * VI;
     float x[VI];
-    if (r < n) {
-      const IT* row = (isq ? qbase : kbase) + (int64_t)(t0 + r) * p.sqk + (int64_t)hk * dk;
-      load_row_vec<IT>(row, e0, dk, p.vec_qk, x);
-    } else {
 #pragma unroll
-      for (int i = 0; i < VI; ++i) x[i] = 0.0f;
-    }
+    for (int i = 0; i < VI; ++i) x[i] = (r < n && e0 + i < dk) ? static_cast<float>(raw[ps][i]) : 0.0f;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < VI; ++i) s += x[i] * x[i];
@@ -121,7 +139,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     for (int i = 0; i < VI; ++i) dst[i] = static_cast<CT>(x[i] * scale);
     if (tid % TPR == 0) (isq ? p.scq : p.invk)[((int64_t)chunk * p.Hk + hk) * kC + r] = scale;
   }
-  __syncthreads();
+  lds_barrier();
 
   // 2. Gram matrices on MFMA: G0 = K K^T, G1 = Q K^T (64 x 64 each).
   {
@@ -141,7 +159,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       for (int i = 0; i < 4; ++i) sG[mat][(tr * 16 + grp * 4 + i) * (kC + 1) + tc * 16 + col] = acc[i];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. per v-head: decay, A (transposed, f32), M, Tm.
   const int rep = p.Hv / p.Hk;
@@ -149,11 +167,10 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     const int nh = min(2, rep - i0);
     if (wave < nh) {
       const int h = hk * rep + i0 + wave;
-      float gv = 0.0f, bv = 0.0f;
-      if (lane < n) {
-        gv = load_scalar(p.g, (int64_t)(t0 + lane) * p.sgb + h, p.dtype_gb);
-        bv = load_scalar(p.beta, (int64_t)(t0 + lane) * p.sgb + h, p.dtype_gb);
-      }
+      const int64_t gi = (int64_t)(t0 + min(lane, n - 1)) * p.sgb + h;
+      const uint32_t gb = load_bits(p.g, gi, p.dtype_gb), bb = load_bits(p.beta, gi, p.dtype_gb);
+      const float gv = lane < n ? bits_to_f32(gb, p.dtype_gb) : 0.0f;
+      const float bv = lane < n ? bits_to_f32(bb, p.dtype_gb) : 0.0f;
       // inclusive prefix sum over the wave (lane = token in chunk)
       float cs = gv;
 #pragma unroll
@@ -165,7 +182,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       sBeta[wave][lane] = bv;
       p.gam[((int64_t)chunk * p.Hv + h) * kC + lane] = cs;
     }
-    __syncthreads();
+    lds_barrier();
     for (int hi = 0; hi < nh; ++hi) {
       const int h = hk * rep + i0 + hi;
       CT* Mout = static_cast<CT*>(p.Mm) + ((int64_t)chunk * p.Hv + h) * kC * kC;
@@ -186,7 +203,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (wave < nh) {
       // Forward substitution for Tm = (I + A)^-1; lane j owns column j.
       const int h = hk * rep + i0 + wave;
@@ -209,12 +226,21 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
 #pragma unroll
       for (int r = 0; r < kC; ++r) Tout[r * kC + lane] = static_cast<CT>(t[r]);
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
 // ---------------------------------------------------------------------------
 // Kernel 2: sequential chunk carry for one (v-head, 16 value columns).
+//
+// Per chunk c (LDS buffer b = c & 1 for the normalised K/Q rows):
+//   stage(c) -> barrier A -> prefetch(c+1) into registers ->
+//   X = [K;Q] S, Y (waves 0,1) | O = exp(gam) Q S (waves 2,3) -> barrier B ->
+//   Delta = Tm Y -> barrier C -> O += M Delta, store | S update.
+// The K^T operand of the state update is gathered from the row-major K rows
+// (strided 2-byte LDS reads) with the per-token decay folded in, so no
+// transposed copy is staged.  Double-buffered K/Q rows remove the barrier
+// that would otherwise guard the next chunk's staging.
 // ---------------------------------------------------------------------------
 template <class CT, class IT, int DK>
 __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
@@ -225,23 +251,23 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   constexpr int EPF = 16 / sizeof(CT);
   constexpr int KB = Mma<CT>::kBlock;
   constexpr int LDK = DK + EPF;   // [token][dk] rows
-  constexpr int LDT = kC + EPF;   // [dk or value][token] rows
+  constexpr int LDT = kC + EPF;   // [value][token] rows
   constexpr int NST = DK / 16;    // state row tiles
   constexpr int SPW = (NST + 3) / 4;  // state tiles per wave
   constexpr int NKB_T = kC / KB;  // k-blocks over tokens
   typedef typename Mma<CT>::frag frag;
+  typedef typename Vec16<IT>::type vecI;
 
-  __shared__ __attribute__((aligned(16))) CT sK[kC * LDK];
-  __shared__ __attribute__((aligned(16))) CT sQ[kC * LDK];
-  __shared__ __attribute__((aligned(16))) CT sKt[DK * LDT];
+  __shared__ __attribute__((aligned(16))) CT sKQ[2][2 * kC * LDK];  // rows 0..63 K, 64..127 Q
   __shared__ __attribute__((aligned(16))) CT sSt[kVT * LDK];
   __shared__ __attribute__((aligned(16))) CT sYt[kVT * LDT];
   __shared__ __attribute__((aligned(16))) CT sDt[kVT * LDT];
-  __shared__ __attribute__((aligned(16))) CT sDw[kVT * LDT];
-  __shared__ __attribute__((aligned(16))) CT sDc[kVT * LDT];
-  __shared__ float sGam[kC], sBeta[kC];
+  __shared__ float sEg[2][kC];    // exp(gam_r)
+  __shared__ float sWl[2][kC];    // exp(gam_last - gam_r)
+  __shared__ float sGam[2][kC];
+  __shared__ float sBeta[2][kC];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int col = lane & 15, grp = lane >> 4;
 
   // XCD-aware placement: logical work-group L -> consecutive L share a k-head.
@@ -255,8 +281,9 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   const int h = hk * rep + rem / ntiles;
   const int j0 = (rem % ntiles) * kVT;
   const int dk = p.dk, dv = p.dv;
-  const int jc = j0 + col;          // this lane's value column
+  const int jc = j0 + col;  // this lane's value column
   const bool col_ok = jc < dv;
+  const int jcc = min(jc, dv - 1);
 
   // ---- state in accumulators: tile s of this wave covers dk rows 16*(wave+4s)..
   float4_t S[SPW];
@@ -267,8 +294,7 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
     for (int i = 0; i < 4; ++i) {
       const int row = tile * 16 + grp * 4 + i;
       float v = 0.0f;
-      if (p.initial && tile < NST && row < dk && col_ok)
-        v = p.initial[((int64_t)h * dk + row) * dv + jc];
+      if (p.initial && tile < NST && row < dk && col_ok) v = p.initial[((int64_t)h * dk + row) * dv + jc];
       S[s][i] = v;
     }
   }
@@ -284,15 +310,17 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   };
   store_state_lds();
 
-  // ---- prefetch registers for one chunk
+  // ---- prefetch registers (raw input dtype; converted at use)
   const IT* qbase = static_cast<const IT*>(p.q);
   const IT* kbase = static_cast<const IT*>(p.k);
-  float raw[NPASS][VI];
+  const IT* vbase = static_cast<const IT*>(p.v);
+  vecI raw[NPASS];
   float rsc[NPASS];
-  frag tfr[NKB_T];          // Tm rows of tile `wave`
-  frag mfr[2][NKB_T];       // M rows (waves 2,3)
-  float vv[2][4];           // V values (waves 0,1)
-  float pg = 0.0f, pb = 0.0f;  // gam / beta of token `lane` (wave 0 / 1)
+  frag tfr[NKB_T];      // Tm rows of tile `wave`
+  frag mfr[2][NKB_T];   // M rows (waves 2,3)
+  IT vraw[2][4];        // V values (waves 0,1)
+  float pg = 0.0f;      // gam of token `lane` (wave 0)
+  uint32_t pb = 0;      // beta bits of token `lane` (wave 1)
 
   auto prefetch = [&](int chunk) {
     const int t0 = chunk * kC;
@@ -301,17 +329,10 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
     for (int ps = 0; ps < NPASS; ++ps) {
       const int rr = ps * RPP + tid / TPR;
       const bool isq = rr >= kC;
-      const int r = isq ? rr - kC : rr;
-      const int e0 = (tid % TPR) * VI;
-      if (r < n) {
-        const IT* row = (isq ? qbase : kbase) + (int64_t)(t0 + r) * p.sqk + (int64_t)hk * dk;
-        load_row_vec<IT>(row, e0, dk, p.vec_qk, raw[ps]);
-        rsc[ps] = (isq ? p.scq : p.invk)[((int64_t)chunk * p.Hk + hk) * kC + r];
-      } else {
-#pragma unroll
-        for (int i = 0; i < VI; ++i) raw[ps][i] = 0.0f;
-        rsc[ps] = 0.0f;
-      }
+      const int r = min(isq ? rr - kC : rr, n - 1);
+      const IT* row = (isq ? qbase : kbase) + (int64_t)(t0 + r) * p.sqk + (int64_t)hk * dk;
+      raw[ps] = load_row_raw<IT>(row, (tid % TPR) * VI, dk, p.vec_qk);
+      rsc[ps] = (isq ? p.scq : p.invk)[((int64_t)chunk * p.Hk + hk) * kC + r];
     }
     const CT* Tm = static_cast<const CT*>(p.Tm) + ((int64_t)chunk * p.Hv + h) * kC * kC;
 #pragma unroll
@@ -329,15 +350,12 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = wave * 32 + s * 16 + grp * 4 + i;
-          vv[s][i] = (r < n && col_ok)
-                         ? load_scalar(p.v, (int64_t)(t0 + r) * p.sv + (int64_t)h * dv + jc, p.dtype_qkv)
-                         : 0.0f;
+          const int r = min(wave * 32 + s * 16 + grp * 4 + i, n - 1);
+          vraw[s][i] = vbase[(int64_t)(t0 + r) * p.sv + (int64_t)h * dv + jcc];
         }
     }
     if (wave == 0) pg = p.gam[((int64_t)chunk * p.Hv + h) * kC + lane];
-    if (wave == 1)
-      pb = lane < n ? load_scalar(p.beta, (int64_t)(t0 + lane) * p.sgb + h, p.dtype_gb) : 0.0f;
+    if (wave == 1) pb = load_bits(p.beta, (int64_t)(t0 + min(lane, n - 1)) * p.sgb + h, p.dtype_gb);
   };
 
   const int nchunks = p.nchunks;
@@ -347,23 +365,26 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   for (int chunk = 0; chunk < nchunks; ++chunk) {
     const int t0 = chunk * kC;
     const int n = min(kC, p.T - t0);
-    // ---- stage: normalised K, Q rows and K^T into LDS
+    const int b = chunk & 1;
+    CT* sK = sKQ[b];
+    // ---- stage: normalised K and Q rows into LDS buffer b
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
       const int rr = ps * RPP + tid / TPR;
-      const bool isq = rr >= kC;
-      const int r = isq ? rr - kC : rr;
+      const int r = rr >= kC ? rr - kC : rr;
       const int e0 = (tid % TPR) * VI;
-      CT* dst = (isq ? sQ : sK) + r * LDK + e0;
+      CT* dst = sKQ[b] + rr * LDK + e0;
 #pragma unroll
-      for (int i = 0; i < VI; ++i) {
-        const CT x = static_cast<CT>(raw[ps][i] * rsc[ps]);
-        dst[i] = x;
-        if (!isq) sKt[(e0 + i) * LDT + r] = x;
-      }
+      for (int i = 0; i < VI; ++i)
+        dst[i] = static_cast<CT>((r < n && e0 + i < dk) ? static_cast<float>(raw[ps][i]) * rsc[ps] : 0.0f);
     }
-    if (wave == 0) sGam[lane] = pg;
-    if (wave == 1) sBeta[lane] = pb;
+    if (wave == 0) {
+      const float gl = __shfl(pg, kC - 1, 64);
+      sGam[b][lane] = pg;
+      sEg[b][lane] = expf(pg);
+      sWl[b][lane] = expf(gl - pg);
+    }
+    if (wave == 1) sBeta[b][lane] = lane < n ? bits_to_f32(pb, p.dtype_gb) : 0.0f;
     frag tcur[NKB_T];
     frag mcur[2][NKB_T];
     float vcur[2][4];
@@ -374,9 +395,12 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
 #pragma unroll
       for (int kb = 0; kb < NKB_T; ++kb) mcur[s][kb] = mfr[s][kb];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vcur[s][i] = vv[s][i];
+      for (int i = 0; i < 4; ++i) {
+        const int r = wave * 32 + s * 16 + grp * 4 + i;
+        vcur[s][i] = (r < n && col_ok) ? static_cast<float>(vraw[s][i]) : 0.0f;
+      }
     }
-    __syncthreads();  // (A) operands of this chunk are in LDS
+    lds_barrier();  // (A) operands of this chunk are in LDS
     if (chunk + 1 < nchunks) prefetch(chunk + 1);
 
     // ---- X = [K; Q] S : wave w -> row tiles 2w, 2w+1 of the 128-row product
@@ -384,18 +408,13 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) X[s] = float4_t{0.f, 0.f, 0.f, 0.f};
     {
-      const CT* srcs[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int xt = wave * 2 + s;
-        srcs[s] = (xt < 4 ? sK : sQ) + ((xt & 3) * 16 + col) * LDK + grp * EPF;
-      }
+      const CT* asrc = sKQ[b] + (wave * 32 + col) * LDK + grp * EPF;
       const CT* bsrc = sSt + col * LDK + grp * EPF;
 #pragma unroll
       for (int kb = 0; kb < DK / KB; ++kb) {
-        const frag b = load_frag<CT>(bsrc + kb * KB);
+        const frag bf = load_frag<CT>(bsrc + kb * KB);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) Mma<CT>::mma(X[s], load_frag<CT>(srcs[s] + kb * KB), b);
+        for (int s = 0; s < 2; ++s) Mma<CT>::mma(X[s], load_frag<CT>(asrc + s * 16 * LDK + kb * KB), bf);
       }
     }
     // ---- waves 0,1: Y = beta (V - exp(gam) K S) -> Y^T in LDS
@@ -404,56 +423,41 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int rbase = (wave & 1) * 32 + s * 16 + grp * 4;
-      float y[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rbase + i;
-        const float eg = expf(sGam[r]);
-        if (wave < 2)
-          y[i] = sBeta[r] * (vcur[s][i] - eg * X[s][i]);
-        else
-          O[s][i] = eg * X[s][i];
-      }
       if (wave < 2) {
+        CT y4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sYt[col * LDT + rbase + i] = static_cast<CT>(y[i]);
+        for (int i = 0; i < 4; ++i) {
+          const int r = rbase + i;
+          y4[i] = static_cast<CT>(sBeta[b][r] * (vcur[s][i] - sEg[b][r] * X[s][i]));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sYt[col * LDT + rbase + i] = y4[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[s][i] = sEg[b][rbase + i] * X[s][i];
       }
     }
-    __syncthreads();  // (B) Y^T ready
+    lds_barrier();  // (B) Y^T ready
 
     // ---- Delta = Tm Y : wave w -> row tile w
-    const float gl = sGam[kC - 1];
     {
       float4_t D = {0.f, 0.f, 0.f, 0.f};
       const CT* bsrc = sYt + col * LDT + grp * EPF;
 #pragma unroll
       for (int kb = 0; kb < NKB_T; ++kb) Mma<CT>::mma(D, tcur[kb], load_frag<CT>(bsrc + kb * KB));
-      const int rbase = wave * 16 + grp * 4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rbase + i;
-        sDt[col * LDT + r] = static_cast<CT>(D[i]);
-        sDw[col * LDT + r] = static_cast<CT>(D[i] * expf(gl - sGam[r]));
-      }
-      if (chunk == cap_chunk) {
-        const float gc = sGam[cap_row];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = rbase + i;
-          sDc[col * LDT + r] = static_cast<CT>(r <= cap_row ? D[i] * expf(gc - sGam[r]) : 0.0f);
-        }
-      }
+      for (int i = 0; i < 4; ++i) sDt[col * LDT + wave * 16 + grp * 4 + i] = static_cast<CT>(D[i]);
     }
-    __syncthreads();  // (C) Delta^T ready
+    lds_barrier();  // (C) Delta^T ready
 
     // ---- waves 2,3: O += M Delta, store
     if (wave >= 2) {
       const CT* bsrc = sDt + col * LDT + grp * EPF;
 #pragma unroll
       for (int kb = 0; kb < NKB_T; ++kb) {
-        const frag b = load_frag<CT>(bsrc + kb * KB);
+        const frag bf = load_frag<CT>(bsrc + kb * KB);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) Mma<CT>::mma(O[s], mcur[s][kb], b);
+        for (int s = 0; s < 2; ++s) Mma<CT>::mma(O[s], mcur[s][kb], bf);
       }
       if (col_ok) {
 #pragma unroll
@@ -466,19 +470,31 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
           }
       }
     }
+    // K^T fragment (dk rows of `tile`, tokens of k-block kb) scaled per token by w.
+    auto kt_frag = [&](int tile, int kb, const float* w) {
+      frag f;
+      const int e = tile * 16 + col;
+#pragma unroll
+      for (int j = 0; j < EPF; ++j) {
+        const int tok = kb * KB + grp * EPF + j;
+        f[j] = static_cast<CT>(static_cast<float>(sK[tok * LDK + e]) * w[tok]);
+      }
+      return f;
+    };
     // ---- optional capture of the state after token `capture`
     if (chunk == cap_chunk) {
-      const float ec = expf(sGam[cap_row]);
+      __shared__ float sWc[kC];
+      if (wave == 0) sWc[lane] = lane <= cap_row ? expf(sGam[b][cap_row] - sGam[b][lane]) : 0.0f;
+      lds_barrier();
+      const float ec = sEg[b][cap_row];
 #pragma unroll
       for (int s = 0; s < SPW; ++s) {
         const int tile = wave + 4 * s;
         if (tile < NST) {
           float4_t acc = S[s] * ec;
-          const CT* asrc = sKt + (tile * 16 + col) * LDT + grp * EPF;
-          const CT* bsrc = sDc + col * LDT + grp * EPF;
+          const CT* bsrc = sDt + col * LDT + grp * EPF;
 #pragma unroll
-          for (int kb = 0; kb < NKB_T; ++kb)
-            Mma<CT>::mma(acc, load_frag<CT>(asrc + kb * KB), load_frag<CT>(bsrc + kb * KB));
+          for (int kb = 0; kb < NKB_T; ++kb) Mma<CT>::mma(acc, kt_frag(tile, kb, sWc), load_frag<CT>(bsrc + kb * KB));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int row = tile * 16 + grp * 4 + i;
@@ -487,24 +503,22 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
         }
       }
     }
-    // ---- S <- exp(gam_last) S + K^T Dw
+    // ---- S <- exp(gam_last) S + (diag(w) K)^T Delta
     {
-      const float el = expf(gl);
+      const float el = sEg[b][kC - 1];
+      const CT* bsrc = sDt + col * LDT + grp * EPF;
 #pragma unroll
       for (int s = 0; s < SPW; ++s) {
         const int tile = wave + 4 * s;
         if (tile < NST) {
           S[s] = S[s] * el;
-          const CT* asrc = sKt + (tile * 16 + col) * LDT + grp * EPF;
-          const CT* bsrc = sDw + col * LDT + grp * EPF;
 #pragma unroll
           for (int kb = 0; kb < NKB_T; ++kb)
-            Mma<CT>::mma(S[s], load_frag<CT>(asrc + kb * KB), load_frag<CT>(bsrc + kb * KB));
+            Mma<CT>::mma(S[s], kt_frag(tile, kb, sWl[b]), load_frag<CT>(bsrc + kb * KB));
         }
       }
     }
     store_state_lds();  // sSt is only read before barrier (B)
-    __syncthreads();    // (D) LDS operands of this chunk are consumed
   }
   if (p.final_state) {
 #pragma unroll

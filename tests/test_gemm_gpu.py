@@ -1,0 +1,119 @@
+"""Projection GEMM parity (y = x W^T) against a plain PyTorch reference.
+
+f16: compared with the f32-accumulated product rounded to half, within one
+half ulp plus 1e-3 (the reference's rule, neural.rs:466-480).  f32: compared
+with an f64 product, relative to the norm of the terms.  SwiGLU: compared with
+the reference's half rounding steps, and with the unfused kernels.
+"""
+import pytest
+import torch
+
+gpu = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def clef():
+    import clef_hip
+    clef_hip.lib()
+    return clef_hip
+
+
+def _inputs(seed, M, N, K, dtype):
+    import workloads
+    return workloads.gemm_inputs(seed, M, N, K, dtype=dtype)
+
+
+def _check_f16(y, x, w):
+    ref = (x.float() @ w.float().T)
+    exp = ref.half().float()
+    err = (y.float() - exp).abs()
+    tol = 1e-3 + exp.abs() * 2.0 ** -10
+    assert (err <= tol).all(), f"max err {err.max().item():.3e}"
+
+
+def _check_f32(y, x, w):
+    ref = x.double() @ w.double().T
+    scale = x.double().abs() @ w.double().abs().T
+    err = (y.double() - ref).abs()
+    assert (err <= 1e-5 * scale + 1e-6).all(), f"max rel err {(err / (scale + 1e-30)).max().item():.3e}"
+
+
+SHAPES = [(1, 1, 1), (17, 73, 65), (139, 129, 128), (17, 73, 4096), (513, 137, 65), (1025, 257, 128)]
+
+
+@gpu
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_gemm_reference_shapes(clef, M, N, K, dtype):
+    """neural.rs:439-480 shapes, including ragged tiles and unaligned K."""
+    x, w = _inputs(7, M, N, K, dtype)
+    y = clef.gemm(x, w)
+    (_check_f16 if dtype == torch.float16 else _check_f32)(y, x, w)
+
+
+@gpu
+@pytest.mark.parametrize("N", [8192, 2048, 6144, 12352])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_gemm_projection_shapes(clef, N, dtype):
+    """M = 2048 tokens, K = 2048 hidden; x ~ N(0,1), W ~ N(0,0.02), seed 1."""
+    x, w = _inputs(1, 2048, N, 2048, dtype)
+    y = clef.gemm(x, w)
+    (_check_f16 if dtype == torch.float16 else _check_f32)(y, x, w)
+
+
+@gpu
+@pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8)])
+def test_gemm_residual_epilogue(clef, M, N, K):
+    x, w = _inputs(3, M, N, K, torch.float16)
+    h = torch.randn((M, N), device="cuda")
+    h0 = h.clone()
+    clef.gemm(x, w, residual=h, out_dtype=torch.float16)
+    prod = (x.float() @ w.float().T).half().float()
+    exp = h0 + prod
+    err = (h - exp).abs()  # one half ulp of the product, plus the f32 add
+    assert (err <= 1e-3 + prod.abs() * 2.0 ** -10 + exp.abs() * 2.0 ** -23).all(), \
+        f"max err {err.max().item():.3e}"
+
+
+@gpu
+def test_gemm_f16_output_from_f32_accumulator_rounds_once(clef):
+    x, w = _inputs(4, 300, 200, 512, torch.float16)
+    y32 = clef.gemm(x, w, out_dtype=torch.float32)
+    y16 = clef.gemm(x, w)
+    assert torch.equal(y32.half(), y16)
+
+
+@gpu
+@pytest.mark.parametrize("M,N,K", [(2048, 6144, 2048), (600, 6144, 2048), (20, 32, 16), (513, 137, 64)])
+def test_swiglu_matches_half_rounding_steps_and_unfused_kernels(clef, M, N, K):
+    import workloads
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((M, K), generator=gen, device="cuda").half()
+    wg = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    wu = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    y = clef.gemm_swiglu(x, wg, wu)
+    g = clef.gemm(x, wg).float()
+    u = clef.gemm(x, wu).float()
+    s = (g / (1.0 + torch.exp(-g))).half().float()
+    unfused = (s * u).half()
+    diff = (y.float() - unfused.float()).abs()
+    ulp = unfused.float().abs().clamp(min=2.0 ** -14) * 2.0 ** -10
+    assert (diff <= ulp).all()
+    assert (diff == 0).float().mean() > 0.999
+    gr = (x.float() @ wg.float().T).half().float()
+    ur = (x.float() @ wu.float().T).half().float()
+    ref = ((gr / (1 + torch.exp(-gr))).half().float() * ur).half().float()
+    err = (y.float() - ref).abs()
+    assert (err <= 1e-3 + ref.abs() * 2.0 ** -9).all(), f"max err {err.max().item():.3e}"
+
+
+@gpu
+def test_swiglu_f32(clef):
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn((333, 256), generator=gen, device="cuda")
+    wg = torch.randn((500, 256), generator=gen, device="cuda") * 0.05
+    wu = torch.randn((500, 256), generator=gen, device="cuda") * 0.05
+    y = clef.gemm_swiglu(x, wg, wu)
+    g = x.double() @ wg.double().T
+    ref = torch.nn.functional.silu(g) * (x.double() @ wu.double().T)
+    assert (y.double() - ref).abs().max().item() < 1e-4

@@ -35,17 +35,8 @@ def _check(actual, expected, precision):
 
 
 def baseline_inputs(seed, T, Hk, Hv, dk, dv, dtype=torch.float32, device="cuda"):
-    """Workload generator of the scan configs: q,k ~ N(0,1) then per-head L2
-    normalised, v ~ N(0,1), beta = sigmoid(N(0,1)), g = -softplus(N(0,1))."""
-    gen = torch.Generator(device=device).manual_seed(seed)
-    q = torch.randn((T, Hk, dk), generator=gen, device=device)
-    k = torch.randn((T, Hk, dk), generator=gen, device=device)
-    v = torch.randn((T, Hv, dv), generator=gen, device=device)
-    beta = torch.sigmoid(torch.randn((T, Hv), generator=gen, device=device))
-    g = -torch.nn.functional.softplus(torch.randn((T, Hv), generator=gen, device=device))
-    q = q / q.norm(dim=-1, keepdim=True)
-    k = k / k.norm(dim=-1, keepdim=True)
-    return [x.to(dtype) for x in (q, k, v, g, beta)]
+    import workloads
+    return workloads.scan_inputs(seed, T, Hk, Hv, dk, dv, dtype=dtype, device=device)
 
 
 def _np(*ts):
