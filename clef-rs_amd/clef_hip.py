@@ -53,9 +53,10 @@ SIGNATURES = {
     "clef_conv_silu": (_i, [_p, _l, _i, _p, _i, _p, _i, _p, _l, _i, _i, _i, _p]),
     "clef_delta_gates": (_i, [_p, _l, _p, _l, _i, _p, _p, _p, _p, _i, _i, _p]),
     "clef_gated_rms_silu": (_i, [_p, _p, _l, _i, _p, _p, _i, _i, _i, _i, _f, _p]),
-    "clef_qk_norm_rotary": (_i, [_p, _l, _i, _p, _p, _i, _i, _i, _i, _i, _d, _i, _i, _i, _f, _p]),
-    "clef_head_major": (_i, [_p, _l, _i, _p, _i, _i, _i, _i, _i, _i, _p]),
-    "clef_attention_gated": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _l, _p, _l, _i, _p]),
+    "clef_qk_norm_rotary": (_i, [_p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _d, _i, _i, _f, _p]),
+    "clef_values_transposed": (_i, [_p, _l, _i, _p, _l, _i, _i, _i, _i, _i, _p]),
+    "clef_attention_gated": (_i, [_p, _l, _p, _l, _p, _l, _i, _i, _i, _i, _i, _i, _p, _l, _l, _p, _l,
+                                  _p]),
     "clef_embed": (_i, [_p, _i, _p, _i, _i, _i, _p, _p]),
     "clef_head_logits": (_i, [_p, _i, _p, _i, _p, _p]),
 }
@@ -209,3 +210,240 @@ def gemm_swiglu(x, wg, wu, out=None):
     _check(lib().clef_gemm_swiglu(_ptr(x), _rows(x, "x"), _ptr(wg), _ptr(wu), _rows(wg, "wg"),
                                   _ptr(y), _rows(y, "y"), M, N, K, _dt(x), _stream()))
     return y
+
+
+# ---------------------------------------------------------------------------
+# Pointwise pieces (thin wrappers used by the parity tests)
+# ---------------------------------------------------------------------------
+def rms_norm(x, w, eps=1e-6, out_dtype=None):
+    rows, width = x.shape
+    y = torch.empty((rows, width), dtype=out_dtype or x.dtype, device=x.device)
+    _check(lib().clef_rms_norm(_ptr(x), _rows(x, "x"), _dt(x), _ptr(w), _ptr(y), width, _dt(y),
+                               rows, width, float(eps), _stream()))
+    return y
+
+
+def conv_silu(x, w, history=None, out_dtype=torch.float32):
+    T, W = x.shape
+    taps = w.reshape(W, -1).shape[1]
+    y = torch.empty((T, W), dtype=out_dtype, device=x.device)
+    hist_rows = 0 if history is None else history.shape[0]
+    _check(lib().clef_conv_silu(_ptr(x), _rows(x, "x"), _dt(x), _ptr(history), hist_rows,
+                                _ptr(w.reshape(W, taps).contiguous()), taps, _ptr(y), W, _dt(y), T, W,
+                                _stream()))
+    return y
+
+
+def delta_gates(a, b, dt, a_log):
+    T, Hv = a.shape
+    g = torch.empty((T, Hv), dtype=torch.float32, device=a.device)
+    beta = torch.empty_like(g)
+    _check(lib().clef_delta_gates(_ptr(a), _rows(a, "a"), _ptr(b), _rows(b, "b"), _dt(a), _ptr(dt),
+                                  _ptr(a_log), _ptr(g), _ptr(beta), T, Hv, _stream()))
+    return g, beta
+
+
+def gated_rms_silu(o, z, w, eps=1e-6, out_dtype=torch.float32):
+    T, Hv, width = o.shape
+    y = torch.empty((T, Hv * width), dtype=out_dtype, device=o.device)
+    _check(lib().clef_gated_rms_silu(_ptr(o), _ptr(z), z.stride(0), _dt(z), _ptr(w), _ptr(y), _dt(y),
+                                     T, Hv, width, float(eps), _stream()))
+    return y
+
+
+def qk_norm_rotary(x, heads, d, w, rot_dim, theta, pos0=0, head_stride=None, eps=1e-6,
+                   out=None, dst_offset=0, out_dtype=None):
+    T = x.shape[0]
+    hs = head_stride or d
+    if out is None:
+        out = torch.empty((heads, T + dst_offset, d), dtype=out_dtype or x.dtype, device=x.device)
+    _check(lib().clef_qk_norm_rotary(_ptr(x), x.stride(0), hs, _dt(x), _ptr(w), _ptr(out), out.shape[1],
+                                     _dt(out), T, heads, d, rot_dim, float(theta), pos0, dst_offset,
+                                     float(eps), _stream()))
+    return out
+
+
+def values_transposed(x, heads, d, ld_tok=None, out=None, dst_offset=0, out_dtype=None):
+    T = x.shape[0]
+    if out is None:
+        ld_tok = ld_tok or max(64, ((T + dst_offset + 63) // 64) * 64)
+        out = torch.zeros((heads, d, ld_tok), dtype=out_dtype or x.dtype, device=x.device)
+    _check(lib().clef_values_transposed(_ptr(x), x.stride(0), _dt(x), _ptr(out), out.shape[2], _dt(out),
+                                        T, heads, d, dst_offset, _stream()))
+    return out
+
+
+def attention_gated(q, k, vt, gate, kn=None):
+    """q [heads, qn, d], k [kvh, kn, d], vt [kvh, d, ldv]; gate [qn, heads, *] view."""
+    heads, qn, d = q.shape
+    kvh, kn_, _ = k.shape
+    kn = kn or kn_
+    y = torch.empty((qn, heads * d), dtype=q.dtype, device=q.device)
+    _check(lib().clef_attention_gated(_ptr(q), qn, _ptr(k), kn_, _ptr(vt), vt.shape[2], _dt(q), heads, kvh,
+                                      qn, kn, d, _ptr(gate), gate.stride(0), gate.stride(1), _ptr(y),
+                                      heads * d, _stream()))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Hybrid backbone (Backbone::{load, prefill}, qwen.rs:193-426)
+# ---------------------------------------------------------------------------
+class BackboneConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "hidden", "intermediate", "vocab", "heads", "kv_heads", "head_dim", "rotary_dim",
+        "lin_k_heads", "lin_v_heads", "lin_dk", "lin_dv", "conv_taps", "n_layers")] + [
+        ("eps", C.c_float), ("rope_theta", C.c_double), ("profile", C.c_int),
+        ("scan_precision", C.c_int), ("max_tokens", C.c_int)]
+
+
+_LW = ("input_norm", "post_norm", "gate", "up", "down", "qkv", "z", "a", "b", "out", "conv", "dt",
+       "a_log", "norm", "q", "k", "v", "o", "q_norm", "k_norm")
+
+
+class LayerWeights(C.Structure):
+    _fields_ = [("kind", C.c_int)] + [(n, C.c_void_p) for n in _LW]
+
+
+SIGNATURES.update({
+    "clef_backbone_create": (_i, [C.POINTER(BackboneConfig), C.POINTER(LayerWeights), _p, _p,
+                                  C.POINTER(C.c_void_p)]),
+    "clef_backbone_destroy": (None, [_p]),
+    "clef_backbone_workspace": (_z, [_p, _i, _i]),
+    "clef_backbone_prefix_bytes": (_z, [_p, _i]),
+    "clef_backbone_prefill": (_i, [_p, C.POINTER(C.c_int32), _i, _p, _i, _i, _p, _p, _p, _z, _p]),
+})
+
+
+class PrefixState:
+    """Device copy of a captured prefix (PrefixState, qwen.rs:153-191)."""
+
+    def __init__(self, buffer, tokens):
+        self.buffer, self.tokens = buffer, tokens
+
+    def bytes(self):
+        return self.buffer.numel()
+
+
+class Backbone:
+    """Hybrid backbone over checkpoint tensors named as the reference names them.
+
+    `weights` maps "model.language_model.*" names to device tensors; matrices
+    are cast to the profile dtype (f16 for "mixed", f32 for "f32") and vectors
+    to f32 here, once.
+    """
+
+    P = "model.language_model."
+
+    def __init__(self, config: dict, weights: dict, profile: str = "f32", scan_precision=None,
+                 max_tokens: int = 4096, device="cuda"):
+        if profile not in ("f32", "mixed"):
+            raise ClefError(-1, "profile must be 'f32' or 'mixed'")
+        self.profile = profile
+        self.dtype = torch.float32 if profile == "f32" else torch.float16
+        if scan_precision is None:
+            scan_precision = "strict" if profile == "f32" else "mixed"
+        rp = config["rope_parameters"]
+        c = BackboneConfig()
+        c.hidden, c.intermediate, c.vocab = config["hidden_size"], config["intermediate_size"], config["vocab_size"]
+        c.heads, c.kv_heads, c.head_dim = (config["num_attention_heads"], config["num_key_value_heads"],
+                                           config["head_dim"])
+        c.rotary_dim = int(config["head_dim"] * rp["partial_rotary_factor"])
+        c.lin_k_heads, c.lin_v_heads = config["linear_num_key_heads"], config["linear_num_value_heads"]
+        c.lin_dk, c.lin_dv = config["linear_key_head_dim"], config["linear_value_head_dim"]
+        c.conv_taps = config["linear_conv_kernel_dim"]
+        c.n_layers = len(config["layer_types"])
+        c.eps, c.rope_theta = config["rms_norm_eps"], rp["rope_theta"]
+        c.profile = 0 if profile == "f32" else 1
+        c.scan_precision = STRICT if scan_precision == "strict" else MIXED
+        c.max_tokens = max_tokens
+        self.c, self.config = c, config
+        self._keep = []
+        P = self.P
+
+        def mat(name):
+            t = weights[name].to(device=device, dtype=self.dtype).contiguous()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        def vec(name):
+            t = weights[name].to(device=device, dtype=torch.float32).contiguous()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        layers = (LayerWeights * c.n_layers)()
+        for i, kind in enumerate(config["layer_types"]):
+            L, p = layers[i], f"{P}layers.{i}."
+            L.input_norm = vec(p + "input_layernorm.weight")
+            L.post_norm = vec(p + "post_attention_layernorm.weight")
+            L.gate, L.up, L.down = (mat(p + f"mlp.{n}_proj.weight") for n in ("gate", "up", "down"))
+            if kind == "full_attention":
+                L.kind = 1
+                a = p + "self_attn."
+                L.q, L.k, L.v, L.o = (mat(a + f"{n}_proj.weight") for n in "qkvo")
+                L.q_norm, L.k_norm = vec(a + "q_norm.weight"), vec(a + "k_norm.weight")
+            else:
+                L.kind = 0
+                a = p + "linear_attn."
+                L.qkv, L.z = mat(a + "in_proj_qkv.weight"), mat(a + "in_proj_z.weight")
+                L.a, L.b = mat(a + "in_proj_a.weight"), mat(a + "in_proj_b.weight")
+                L.out = mat(a + "out_proj.weight")
+                L.conv, L.dt, L.a_log = vec(a + "conv1d.weight"), vec(a + "dt_bias"), vec(a + "A_log")
+                L.norm = vec(a + "norm.weight")
+        emb = mat(P + "embed_tokens.weight")
+        fin = vec(P + "norm.weight")
+        handle = C.c_void_p()
+        L = lib()
+        _declare(L)
+        _check(L.clef_backbone_create(C.byref(c), layers, emb, fin, C.byref(handle)))
+        self._h = handle
+        self._ws = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None):
+                lib().clef_backbone_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+    def _workspace(self, T, prefix, device):
+        n = lib().clef_backbone_workspace(self._h, T, prefix)
+        if n == 0:
+            raise ClefError(-1, "backbone workspace")
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = torch.empty(n, dtype=torch.uint8, device=device)
+        return self._ws
+
+    def prefix_bytes(self, tokens):
+        return lib().clef_backbone_prefix_bytes(self._h, tokens)
+
+    def prefill(self, ids, initial: PrefixState = None, capture: int = 0, hidden=None):
+        """Returns (hidden f32 [(prefix + T), H], PrefixState or None)."""
+        import numpy as np
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        T = int(ids.shape[0])
+        prefix = initial.tokens if initial is not None else 0
+        dev = torch.device("cuda", torch.cuda.current_device())
+        if hidden is None:
+            hidden = torch.empty((prefix + T, self.c.hidden), dtype=torch.float32, device=dev)
+        saved = None
+        if capture:
+            nb = self.prefix_bytes(capture)
+            if nb == 0:
+                raise ClefError(-1, "prefill boundary or vocabulary")
+            saved = PrefixState(torch.empty(nb, dtype=torch.uint8, device=dev), capture)
+        ws = self._workspace(T, prefix, dev)
+        _check(lib().clef_backbone_prefill(
+            self._h, ids.ctypes.data_as(C.POINTER(C.c_int32)), T,
+            _ptr(initial.buffer) if initial is not None else None, prefix, int(capture),
+            _ptr(saved.buffer) if saved is not None else None, _ptr(hidden), _ptr(ws), ws.numel(),
+            _stream()))
+        return hidden, saved
+
+
+def head_logits(x_row, w):
+    """logits[j] = x . w[j] (f32), the pooled last-token head."""
+    n, H = w.shape
+    out = torch.empty(n, dtype=torch.float32, device=x_row.device)
+    _check(lib().clef_head_logits(_ptr(x_row), H, _ptr(w), n, _ptr(out), _stream()))
+    return out

@@ -1,0 +1,426 @@
+// Host orchestration of the hybrid prefill: the C++ counterpart of
+// Backbone::{load, prefill} (crates/core/src/models/qwen.rs:193-426), with
+// Delta::forward (:589-688) and FullAttention::forward (:451-525) issuing the
+// gfx950 kernels of this library on one stream.  Nothing here touches tensor
+// values on the host; the only host/device transfer is the token ids.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/clef_hip.h"
+#include "common.hpp"
+
+namespace clef {
+namespace {
+
+size_t al256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// y[r, c] = f32(x[r, c]) for rows of `cols` (conv history capture).
+__global__ void rows_to_f32(const void* x, int64_t ldx, int dtype, float* y, int rows, int cols) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * cols) return;
+  const int r = static_cast<int>(i / cols), c = static_cast<int>(i % cols);
+  const int64_t s = (int64_t)r * ldx + c;
+  y[i] = dtype == CLEF_F32 ? static_cast<const float*>(x)[s] : static_cast<float>(static_cast<const half_t*>(x)[s]);
+}
+
+// y = x + 1 (offset norms, normalization.rs:44-45), or a plain f32 copy.
+__global__ void norm_weight(const float* x, float* y, int n, float add) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = x[i] + add;
+}
+
+}  // namespace
+
+struct LayerState {
+  int kind = 0;
+  // owned
+  void* in_w = nullptr;        // fused [qkv | z | a | b] or [q | k | v], act dtype
+  float* in_norm = nullptr;    // input_norm offset
+  float* post_norm = nullptr;  // post_attention_layernorm offset
+  float* conv = nullptr;       // [W, taps]
+  float* dt = nullptr;
+  float* a_log = nullptr;
+  float* gnorm = nullptr;      // gated norm (no offset)
+  float* q_norm = nullptr;     // offset
+  float* k_norm = nullptr;     // offset
+  // referenced
+  const void* gate = nullptr;
+  const void* up = nullptr;
+  const void* down = nullptr;
+  const void* out = nullptr;   // DeltaNet out_proj or attention o_proj
+};
+
+}  // namespace clef
+
+struct clef_backbone {
+  clef_backbone_config c;
+  std::vector<clef::LayerState> layers;
+  const void* embeddings = nullptr;
+  float* final_norm = nullptr;
+  std::vector<void*> owned;
+  int ad = CLEF_F32;      // activation / projection dtype
+  int conv_dt = CLEF_F32; // dtype of the conv output fed to the scan
+  int key = 0, value = 0, W = 0, NP = 0, NA = 0;  // widths
+};
+
+namespace clef {
+namespace {
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(static_cast<int>(e), std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct Workspace {
+  int32_t* ids;
+  void* n;        // [T, H] act
+  void* proj;     // [T, max(NP, NA)] act
+  void* mixed;    // [T, W] conv_dt
+  float* g;       // [T, Hv]
+  float* beta;    // [T, Hv]
+  float* scan_out;  // [T, Hv*dv]
+  void* gated;    // [T, max(value, heads*d)] act
+  void* mlp;      // [T, I] act
+  void* qh;       // [heads, T, d] act
+  void* kh;       // [kvh, Ttot, d] act
+  void* vt;       // [kvh, d, ldv] act
+  void* scan_ws;
+  size_t scan_ws_bytes;
+  int ldv;
+};
+
+size_t elt(int dtype) { return dtype == CLEF_F32 ? 4 : 2; }
+
+size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base) {
+  const clef_backbone_config& c = b->c;
+  const size_t a = elt(b->ad);
+  const int Ttot = prefix + T;
+  const int ldv = static_cast<int>(((Ttot + 63) / 64) * 64);
+  const size_t scan_ws = clef_delta_scan_workspace(T, c.lin_k_heads, c.lin_v_heads, c.lin_dk, c.lin_dv, 64,
+                                                   c.scan_precision);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += al256(bytes);
+    return static_cast<void*>(p);
+  };
+  Workspace tmp{};
+  Workspace& W = w ? *w : tmp;
+  const int proj_cols = b->NP > b->NA ? b->NP : b->NA;
+  const int gated_cols = b->value > c.heads * c.head_dim ? b->value : c.heads * c.head_dim;
+  W.ids = static_cast<int32_t*>(take(sizeof(int32_t) * T));
+  W.n = take(a * T * c.hidden);
+  W.proj = take(a * T * proj_cols);
+  W.mixed = take(elt(b->conv_dt) * T * b->W);
+  W.g = static_cast<float*>(take(4ull * T * c.lin_v_heads));
+  W.beta = static_cast<float*>(take(4ull * T * c.lin_v_heads));
+  W.scan_out = static_cast<float*>(take(4ull * T * b->value));
+  W.gated = take(a * T * gated_cols);
+  W.mlp = take(a * T * c.intermediate);
+  W.qh = take(a * (size_t)c.heads * T * c.head_dim);
+  W.kh = take(a * (size_t)c.kv_heads * Ttot * c.head_dim);
+  W.vt = take(a * (size_t)c.kv_heads * c.head_dim * ldv);
+  W.scan_ws = take(scan_ws);
+  W.scan_ws_bytes = scan_ws;
+  W.ldv = ldv;
+  return off;
+}
+
+// Prefix-state layout: hidden [tokens, H] f32, then per layer either
+// recurrent [Hv, dk, dv] f32 + history [taps-1, W] f32, or keys
+// [kvh, tokens, d] + values [kvh, d, tokens] in the activation dtype.
+struct PrefixView {
+  float* hidden;
+  std::vector<float*> rec, hist;
+  std::vector<void*> key, val;
+};
+
+size_t prefix_layout(const clef_backbone* b, int tokens, char* base, PrefixView* v) {
+  const clef_backbone_config& c = b->c;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += al256(bytes);
+    return p;
+  };
+  PrefixView tmp;
+  PrefixView& P = v ? *v : tmp;
+  P.rec.assign(c.n_layers, nullptr);
+  P.hist.assign(c.n_layers, nullptr);
+  P.key.assign(c.n_layers, nullptr);
+  P.val.assign(c.n_layers, nullptr);
+  P.hidden = reinterpret_cast<float*>(take(4ull * tokens * c.hidden));
+  for (int i = 0; i < c.n_layers; ++i) {
+    if (b->layers[i].kind == 0) {
+      P.rec[i] = reinterpret_cast<float*>(take(4ull * c.lin_v_heads * c.lin_dk * c.lin_dv));
+      P.hist[i] = reinterpret_cast<float*>(take(4ull * (c.conv_taps - 1) * b->W));
+    } else {
+      P.key[i] = take(elt(b->ad) * (size_t)c.kv_heads * tokens * c.head_dim);
+      P.val[i] = take(elt(b->ad) * (size_t)c.kv_heads * c.head_dim * tokens);
+    }
+  }
+  return off;
+}
+
+#define CLEF_TRY(expr)        \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_ != 0) return rc_; \
+  } while (0)
+#define HIP_TRY(expr, what)                          \
+  do {                                               \
+    hipError_t e_ = (expr);                          \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+int copy_rows(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return 0;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s), "device copy");
+  return 0;
+}
+
+}  // namespace
+}  // namespace clef
+
+using namespace clef;
+
+extern "C" int clef_backbone_create(const clef_backbone_config* config, const clef_layer_weights* lw,
+                                    const void* embeddings, const void* final_norm,
+                                    clef_backbone** out) {
+  CLEF_REQUIRE(config && lw && embeddings && final_norm && out, "backbone: null argument");
+  const clef_backbone_config& c = *config;
+  CLEF_REQUIRE(c.hidden >= 1 && c.intermediate >= 1 && c.vocab >= 1 && c.n_layers >= 1,
+               "backbone: hidden, intermediate, vocab and layer count must be positive");
+  CLEF_REQUIRE(c.profile == CLEF_PROFILE_F32 || c.profile == CLEF_PROFILE_MIXED_F16, "backbone: profile");
+  CLEF_REQUIRE(c.scan_precision == CLEF_SCAN_STRICT || c.scan_precision == CLEF_SCAN_MIXED,
+               "backbone: scan precision");
+  CLEF_REQUIRE(c.eps > 0.0f && c.eps <= 1.0f, "backbone: epsilon");
+  CLEF_REQUIRE(c.max_tokens >= 1 && c.max_tokens <= (1 << 20), "backbone: max_tokens");
+  bool any_attn = false, any_delta = false;
+  for (int i = 0; i < c.n_layers; ++i) {
+    CLEF_REQUIRE(lw[i].kind == 0 || lw[i].kind == 1, "backbone: layer kind");
+    (lw[i].kind ? any_attn : any_delta) = true;
+  }
+  if (any_delta)
+    CLEF_REQUIRE(c.lin_k_heads >= 1 && c.lin_v_heads % c.lin_k_heads == 0 && c.lin_dk >= 1 &&
+                     c.lin_dk <= 128 && c.lin_dv >= 1 && c.lin_dv <= 128 && c.conv_taps >= 1 &&
+                     c.conv_taps <= 8,
+                 "backbone: DeltaNet head layout");
+  if (any_attn)
+    CLEF_REQUIRE(c.heads >= 1 && c.kv_heads >= 1 && c.heads % c.kv_heads == 0 && c.head_dim >= 1 &&
+                     c.head_dim <= 256 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim &&
+                     c.head_dim % (c.profile == CLEF_PROFILE_F32 ? 4 : 8) == 0,
+                 "backbone: attention head layout");
+
+  std::unique_ptr<clef_backbone> b(new (std::nothrow) clef_backbone());
+  CLEF_REQUIRE(b, "backbone: out of host memory");
+  b->c = c;
+  if (!any_delta) b->c.lin_k_heads = b->c.lin_v_heads = b->c.lin_dk = b->c.lin_dv = 1, b->c.conv_taps = 1;
+  if (!any_attn) b->c.heads = b->c.kv_heads = 1, b->c.head_dim = 8, b->c.rotary_dim = 0;
+  const clef_backbone_config& C = b->c;
+  b->ad = c.profile == CLEF_PROFILE_F32 ? CLEF_F32 : CLEF_F16;
+  b->conv_dt = (c.profile == CLEF_PROFILE_F32 || c.scan_precision == CLEF_SCAN_STRICT) ? CLEF_F32 : CLEF_F16;
+  b->key = C.lin_k_heads * C.lin_dk;
+  b->value = C.lin_v_heads * C.lin_dv;
+  b->W = 2 * b->key + b->value;
+  b->NP = b->W + b->value + 2 * C.lin_v_heads;
+  b->NA = 2 * C.heads * C.head_dim + 2 * C.kv_heads * C.head_dim;
+  b->embeddings = embeddings;
+  const size_t a = elt(b->ad);
+  const int H = C.hidden;
+
+  auto alloc = [&](size_t bytes) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    b->owned.push_back(p);
+    return p;
+  };
+  auto offset_norm = [&](const void* src, int n, float add) -> float* {
+    float* dst = static_cast<float*>(alloc(4ull * n));
+    if (!dst) return nullptr;
+    hipLaunchKernelGGL(norm_weight, dim3((n + 255) / 256), dim3(256), 0, 0, static_cast<const float*>(src), dst,
+                       n, add);
+    return dst;
+  };
+  auto cleanup = [&]() {
+    for (void* p : b->owned) (void)hipFree(p);
+    b->owned.clear();
+  };
+  b->final_norm = offset_norm(final_norm, H, 1.0f);
+  if (!b->final_norm) return cleanup(), fail(-2, "backbone: device allocation failed");
+  for (int i = 0; i < c.n_layers; ++i) {
+    const clef_layer_weights& L = lw[i];
+    LayerState S;
+    S.kind = L.kind;
+    if (!L.input_norm || !L.post_norm || !L.gate || !L.up || !L.down)
+      return cleanup(), fail(-1, "backbone: missing norm or MLP weights");
+    S.in_norm = offset_norm(L.input_norm, H, 1.0f);
+    S.post_norm = offset_norm(L.post_norm, H, 1.0f);
+    S.gate = L.gate;
+    S.up = L.up;
+    S.down = L.down;
+    if (L.kind == 0) {
+      if (!L.qkv || !L.z || !L.a || !L.b || !L.out || !L.conv || !L.dt || !L.a_log || !L.norm)
+        return cleanup(), fail(-1, "backbone: missing DeltaNet weights");
+      // fused in-projection [qkv | z | a | b]: one GEMM over x
+      char* w = static_cast<char*>(alloc(a * (size_t)b->NP * H));
+      if (!w) return cleanup(), fail(-2, "backbone: device allocation failed");
+      size_t o = 0;
+      for (auto [src, rows] : {std::pair<const void*, int>{L.qkv, b->W}, {L.z, b->value},
+                               {L.a, C.lin_v_heads}, {L.b, C.lin_v_heads}}) {
+        if (hipMemcpy(w + o, src, a * (size_t)rows * H, hipMemcpyDeviceToDevice) != hipSuccess)
+          return cleanup(), fail(-2, "backbone: weight copy failed");
+        o += a * (size_t)rows * H;
+      }
+      S.in_w = w;
+      S.out = L.out;
+      S.conv = offset_norm(L.conv, b->W * C.conv_taps, 0.0f);
+      S.dt = offset_norm(L.dt, C.lin_v_heads, 0.0f);
+      S.a_log = offset_norm(L.a_log, C.lin_v_heads, 0.0f);
+      S.gnorm = offset_norm(L.norm, C.lin_dv, 0.0f);
+    } else {
+      if (!L.q || !L.k || !L.v || !L.o || !L.q_norm || !L.k_norm)
+        return cleanup(), fail(-1, "backbone: missing attention weights");
+      char* w = static_cast<char*>(alloc(a * (size_t)b->NA * H));
+      if (!w) return cleanup(), fail(-2, "backbone: device allocation failed");
+      size_t o = 0;
+      const int qrows = 2 * C.heads * C.head_dim, kvrows = C.kv_heads * C.head_dim;
+      for (auto [src, rows] : {std::pair<const void*, int>{L.q, qrows}, {L.k, kvrows}, {L.v, kvrows}}) {
+        if (hipMemcpy(w + o, src, a * (size_t)rows * H, hipMemcpyDeviceToDevice) != hipSuccess)
+          return cleanup(), fail(-2, "backbone: weight copy failed");
+        o += a * (size_t)rows * H;
+      }
+      S.in_w = w;
+      S.out = L.o;
+      S.q_norm = offset_norm(L.q_norm, C.head_dim, 1.0f);
+      S.k_norm = offset_norm(L.k_norm, C.head_dim, 1.0f);
+    }
+    b->layers.push_back(S);
+  }
+  if (hipDeviceSynchronize() != hipSuccess) return cleanup(), fail(-2, "backbone: weight preparation failed");
+  *out = b.release();
+  return 0;
+}
+
+extern "C" void clef_backbone_destroy(clef_backbone* b) {
+  if (!b) return;
+  for (void* p : b->owned) (void)hipFree(p);
+  delete b;
+}
+
+extern "C" size_t clef_backbone_workspace(const clef_backbone* b, int T, int prefix_tokens) {
+  if (!b || T < 1 || prefix_tokens < 0) return 0;
+  return carve(b, T, prefix_tokens, nullptr, nullptr) + 256;
+}
+
+extern "C" size_t clef_backbone_prefix_bytes(const clef_backbone* b, int tokens) {
+  if (!b || tokens < 1) return 0;
+  return prefix_layout(b, tokens, nullptr, nullptr);
+}
+
+extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T, const void* initial,
+                                     int initial_tokens, int capture, void* saved, float* hidden,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  CLEF_REQUIRE(b && ids && hidden && workspace, "prefill: null argument");
+  const clef_backbone_config& c = b->c;
+  const int offset = initial ? initial_tokens : 0;
+  // request validation, qwen.rs:345-359
+  CLEF_REQUIRE(T >= 1 && offset >= 0 && (!initial || offset >= 1) && (int64_t)offset + T <= c.max_tokens,
+               "prefill boundary or vocabulary");
+  CLEF_REQUIRE(capture >= 0 && (capture == 0 || capture < T) && !(initial && capture) &&
+                   (capture == 0 || saved),
+               "prefill boundary or vocabulary");
+  for (int t = 0; t < T; ++t) CLEF_REQUIRE(ids[t] >= 0 && ids[t] < c.vocab, "prefill boundary or vocabulary");
+  const size_t need = carve(b, T, offset, nullptr, nullptr);
+  char* base = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(workspace) + 255) & ~static_cast<uintptr_t>(255));
+  CLEF_REQUIRE(workspace_bytes >= need + static_cast<size_t>(base - static_cast<char*>(workspace)),
+               "prefill: workspace too small");
+  Workspace w;
+  carve(b, T, offset, &w, base);
+  PrefixView init, sav;
+  if (initial) prefix_layout(b, offset, static_cast<char*>(const_cast<void*>(initial)), &init);
+  if (capture) prefix_layout(b, capture, static_cast<char*>(saved), &sav);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int H = c.hidden, ad = b->ad;
+  const size_t a = elt(ad);
+  float* h = hidden + (size_t)offset * H;  // residual stream of the new tokens
+  HIP_TRY(hipMemcpyAsync(w.ids, ids, sizeof(int32_t) * T, hipMemcpyHostToDevice, s), "ids upload");
+  CLEF_TRY(clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
+  const int Hv = c.lin_v_heads, dv = c.lin_dv, taps = c.conv_taps;
+  const int heads = c.heads, kvh = c.kv_heads, d = c.head_dim;
+  const int Ttot = offset + T;
+
+  for (int li = 0; li < c.n_layers; ++li) {
+    const LayerState& L = b->layers[li];
+    CLEF_TRY(clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
+    if (L.kind == 0) {
+      const int NP = b->NP, Wc = b->W;
+      char* proj = static_cast<char*>(w.proj);
+      CLEF_TRY(clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NP, H, ad, ad, CLEF_EPI_STORE, s));
+      const int hist_rows = initial ? (offset < taps - 1 ? offset : taps - 1) : 0;
+      CLEF_TRY(clef_conv_silu(proj, NP, ad, initial ? init.hist[li] : nullptr, hist_rows, L.conv, taps, w.mixed,
+                              Wc, b->conv_dt, T, Wc, s));
+      CLEF_TRY(clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt,
+                                L.a_log, w.g, w.beta, T, Hv, s));
+      const char* mixed = static_cast<const char*>(w.mixed);
+      const size_t ce = elt(b->conv_dt);
+      CLEF_TRY(clef_delta_scan(mixed, mixed + ce * b->key, mixed + ce * 2 * b->key, Wc, Wc, b->conv_dt, w.g,
+                               w.beta, Hv, CLEF_F32, T, c.lin_k_heads, Hv, c.lin_dk, dv, 64, c.scan_precision,
+                               initial ? init.rec[li] : nullptr, capture, w.scan_out, (int64_t)Hv * dv,
+                               CLEF_F32, capture ? sav.rec[li] : nullptr, nullptr, w.scan_ws,
+                               w.scan_ws_bytes, s));
+      CLEF_TRY(clef_gated_rms_silu(w.scan_out, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
+      CLEF_TRY(clef_gemm(w.gated, b->value, L.out, b->value, h, H, T, H, b->value, ad, ad, CLEF_EPI_RESIDUAL, s));
+      if (capture) {  // conv history: last min(capture, taps-1) projected rows (qwen.rs:677-685)
+        const int count = capture < taps - 1 ? capture : taps - 1;
+        if (count > 0) {
+          hipLaunchKernelGGL(rows_to_f32, dim3((count * Wc + 255) / 256), dim3(256), 0, s,
+                             proj + a * (size_t)(capture - count) * NP, (int64_t)NP, ad, sav.hist[li], count, Wc);
+          CLEF_TRY(check_launch("history capture"));
+        }
+      }
+    } else {
+      const int NA = b->NA;
+      char* proj = static_cast<char*>(w.proj);
+      CLEF_TRY(clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
+      const size_t koff = a * 2 * heads * d, voff = koff + a * kvh * d;
+      CLEF_TRY(clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
+                                   c.rope_theta, offset, 0, c.eps, s));
+      if (initial) {  // cached keys and values precede the new ones (qwen.rs:486-496)
+        for (int g = 0; g < kvh; ++g)
+          CLEF_TRY(copy_rows(static_cast<char*>(w.kh) + a * (size_t)g * Ttot * d,
+                             static_cast<char*>(init.key[li]) + a * (size_t)g * offset * d, a * (size_t)offset * d, s));
+        HIP_TRY(hipMemcpy2DAsync(w.vt, a * w.ldv, init.val[li], a * offset, a * offset, (size_t)kvh * d,
+                                 hipMemcpyDeviceToDevice, s),
+                "value prefix copy");
+      }
+      CLEF_TRY(clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
+                                   c.rope_theta, offset, offset, c.eps, s));
+      CLEF_TRY(clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, offset, s));
+      if (capture) {
+        for (int g = 0; g < kvh; ++g)
+          CLEF_TRY(copy_rows(static_cast<char*>(sav.key[li]) + a * (size_t)g * capture * d,
+                             static_cast<char*>(w.kh) + a * (size_t)g * Ttot * d, a * (size_t)capture * d, s));
+        HIP_TRY(hipMemcpy2DAsync(sav.val[li], a * capture, w.vt, a * w.ldv, a * capture, (size_t)kvh * d,
+                                 hipMemcpyDeviceToDevice, s),
+                "value capture");
+      }
+      CLEF_TRY(clef_attention_gated(w.qh, T, w.kh, Ttot, w.vt, w.ldv, ad, heads, kvh, T, Ttot, d, proj + a * d,
+                                    NA, 2 * d, w.gated, (int64_t)heads * d, s));
+      CLEF_TRY(clef_gemm(w.gated, heads * d, L.out, heads * d, h, H, T, H, heads * d, ad, ad, CLEF_EPI_RESIDUAL, s));
+    }
+    CLEF_TRY(clef_rms_norm(h, H, CLEF_F32, L.post_norm, w.n, H, ad, T, H, c.eps, s));
+    CLEF_TRY(clef_gemm_swiglu(w.n, H, L.gate, L.up, H, w.mlp, c.intermediate, T, c.intermediate, H, ad, s));
+    CLEF_TRY(clef_gemm(w.mlp, c.intermediate, L.down, c.intermediate, h, H, T, H, c.intermediate, ad, ad,
+                       CLEF_EPI_RESIDUAL, s));
+  }
+  CLEF_TRY(clef_rms_norm(h, H, CLEF_F32, b->final_norm, h, H, CLEF_F32, T, H, c.eps, s));
+  if (initial) CLEF_TRY(copy_rows(hidden, init.hidden, 4ull * offset * H, s));
+  if (capture) CLEF_TRY(copy_rows(sav.hidden, h, 4ull * capture * H, s));
+  return 0;
+}

@@ -1,0 +1,307 @@
+// Memory-bound pieces around the scan and the attention core, with their C ABI
+// entry points.  Each kernel keeps the reference's op order and rounding
+// points (crates/core/src/models/qwen.rs, ops.rs, pointwise.metal); the
+// multiply/add pairs that the reference rounds separately use __fmul_rn /
+// __fadd_rn so the compiler cannot contract them into FMAs.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <vector>
+
+#include "../../include/clef_hip.h"
+#include "common.hpp"
+
+namespace clef {
+namespace {
+
+__device__ __forceinline__ float ld(const void* p, int64_t i, int dtype) {
+  return dtype == CLEF_F32 ? static_cast<const float*>(p)[i]
+                           : static_cast<float>(static_cast<const half_t*>(p)[i]);
+}
+__device__ __forceinline__ void st(void* p, int64_t i, int dtype, float v) {
+  if (dtype == CLEF_F32)
+    static_cast<float*>(p)[i] = v;
+  else
+    static_cast<half_t*>(p)[i] = static_cast<half_t>(v);
+}
+__device__ __forceinline__ float rnd(float v, int dtype) {
+  return dtype == CLEF_F16 ? static_cast<float>(static_cast<half_t>(v)) : v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---- RMSNorm: one wave per row (ops.rs:17-32; pointwise.metal:7-43) --------
+__global__ __launch_bounds__(256) void rms_kernel(const void* x, int64_t ldx, int dti, const float* w,
+                                                  void* y, int64_t ldy, int dto, int rows, int width,
+                                                  float eps, float inv_width) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float s = 0.0f;
+  for (int i = lane; i < width; i += 64) {
+    const float v = ld(x, (int64_t)row * ldx + i, dti);
+    s += v * v;
+  }
+  s = wave_sum(s);
+  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  for (int i = lane; i < width; i += 64) {
+    const float v = ld(x, (int64_t)row * ldx + i, dti);
+    st(y, (int64_t)row * ldy + i, dto, __fmul_rn(__fmul_rn(v, inverse), w[i]));
+  }
+}
+
+// ---- causal conv + SiLU (qwen.rs:609-618, 765-796) --------------------------
+__global__ __launch_bounds__(256) void conv_silu_kernel(const void* x, int64_t ldx, int dti,
+                                                        const float* hist, int hrows, const float* w,
+                                                        int taps, void* y, int64_t ldy, int dto, int T,
+                                                        int W) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)T * W) return;
+  const int t = static_cast<int>(idx / W), c = static_cast<int>(idx % W);
+  const int pos = hrows + t;  // position in [history; x]
+  float acc = 0.0f;
+  for (int tap = 0; tap < taps; ++tap) {
+    const int src = pos - (taps - 1 - tap);
+    if (src < 0) continue;
+    const float v = src < hrows ? hist[(int64_t)src * W + c] : ld(x, (int64_t)(src - hrows) * ldx + c, dti);
+    acc = __fadd_rn(acc, __fmul_rn(v, w[(int64_t)c * taps + tap]));
+  }
+  st(y, (int64_t)t * ldy + c, dto, acc / (1.0f + expf(-acc)));
+}
+
+// ---- decay and write strength (qwen.rs:619-627) -----------------------------
+__global__ __launch_bounds__(256) void gates_kernel(const void* a, int64_t lda, const void* b,
+                                                    int64_t ldb, int dti, const float* dt,
+                                                    const float* alog, float* g, float* beta, int T,
+                                                    int Hv) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= T * Hv) return;
+  const int t = idx / Hv, h = idx % Hv;
+  const float av = __fadd_rn(ld(a, (int64_t)t * lda + h, dti), dt[h]);
+  const float sp = __fadd_rn(fmaxf(av, 0.0f), logf(__fadd_rn(expf(-fabsf(av)), 1.0f)));
+  g[idx] = __fmul_rn(sp, -expf(alog[h]));
+  beta[idx] = 1.0f / (1.0f + expf(-ld(b, (int64_t)t * ldb + h, dti)));
+}
+
+// ---- gated output norm (qwen.rs:671-676): one wave per (token, head) row ----
+__global__ __launch_bounds__(256) void gated_rms_kernel(const float* o, const void* z, int64_t ldz,
+                                                        int dtz, const float* w, void* y, int dto,
+                                                        int T, int Hv, int width, float eps,
+                                                        float inv_width) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T * Hv) return;
+  const int t = row / Hv, h = row % Hv;
+  float s = 0.0f;
+  for (int i = lane; i < width; i += 64) {
+    const float v = rnd(o[(int64_t)row * width + i], dto);
+    s += v * v;
+  }
+  s = wave_sum(s);
+  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  for (int i = lane; i < width; i += 64) {
+    const float v = rnd(o[(int64_t)row * width + i], dto);
+    const float n = rnd(__fmul_rn(__fmul_rn(v, inverse), w[i]), dto);
+    const float zv = ld(z, (int64_t)t * ldz + (int64_t)h * width + i, dtz);
+    st(y, (int64_t)row * width + i, dto, __fmul_rn(n, zv / (1.0f + expf(-zv))));
+  }
+}
+
+// ---- q/k head norm + rotary, head-major output (qwen.rs:437-470) ------------
+struct RotaryTable {
+  float inv_freq[128];
+};
+
+__global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int64_t ldx, int64_t hs,
+                                                             int dti, const float* w, void* y,
+                                                             int64_t ldy_tok, int dto, int T,
+                                                             int heads, int d, int rot, int pos0,
+                                                             int dst_offset, float eps,
+                                                             float inv_width, RotaryTable tab) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);  // (t, head)
+  const int lane = threadIdx.x & 63;
+  if (row >= T * heads) return;
+  const int t = row / heads, h = row % heads;
+  const int64_t src = (int64_t)t * ldx + (int64_t)h * hs;
+  float s = 0.0f;
+  for (int i = lane; i < d; i += 64) {
+    const float v = ld(x, src + i, dti);
+    s += v * v;
+  }
+  s = wave_sum(s);
+  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  const int half = rot / 2;
+  const float p = static_cast<float>(pos0 + t);
+  const int64_t dst = ((int64_t)h * ldy_tok + dst_offset + t) * d;
+  for (int i = lane; i < d; i += 64) {
+    const float v = rnd(__fmul_rn(__fmul_rn(ld(x, src + i, dti), inverse), w[i]), dto);
+    float out = v;
+    if (i < rot) {
+      const int j = i < half ? i + half : i - half;
+      const float vj = rnd(__fmul_rn(__fmul_rn(ld(x, src + j, dti), inverse), w[j]), dto);
+      const float r = i < half ? -vj : vj;
+      const float ang = __fmul_rn(p, tab.inv_freq[i % half]);
+      out = __fadd_rn(__fmul_rn(v, cosf(ang)), __fmul_rn(r, sinf(ang)));
+    }
+    st(y, dst + i, dto, out);
+  }
+}
+
+// ---- values to [heads, d, tokens] --------------------------------------------
+__global__ __launch_bounds__(256) void values_t_kernel(const void* x, int64_t ldx, int dti, void* y,
+                                                       int64_t ldy_tok, int dto, int T, int heads,
+                                                       int d, int dst_offset) {
+  // tile of 64 tokens x 64 features per block, transposed through LDS
+  __shared__ float tile[64][65];
+  const int h = blockIdx.z, t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int t = t0 + r, e = e0 + tx;
+    tile[r][tx] = (t < T && e < d) ? ld(x, (int64_t)t * ldx + (int64_t)h * d + e, dti) : 0.0f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int e = e0 + r, t = t0 + tx;
+    if (t < T && e < d) st(y, ((int64_t)h * d + e) * ldy_tok + dst_offset + t, dto, tile[tx][r]);
+  }
+}
+
+// ---- embedding gather and pooled head ---------------------------------------
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, int T, const void* table, int dt,
+                                                    int vocab, int H, float* h) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)T * H) return;
+  const int t = static_cast<int>(idx / H), c = static_cast<int>(idx % H);
+  const int id = min(max(ids[t], 0), vocab - 1);  // ids are validated by the caller
+  h[idx] = ld(table, (int64_t)id * H + c, dt);
+}
+
+__global__ __launch_bounds__(64) void head_kernel(const float* x, int H, const float* w, float* logits) {
+  const int j = blockIdx.x, lane = threadIdx.x;
+  float s = 0.0f;
+  for (int i = lane; i < H; i += 64) s += x[i] * w[(int64_t)j * H + i];
+  s = wave_sum(s);
+  if (lane == 0) logits[j] = s;
+}
+
+bool dtype_ok(int d) { return d == CLEF_F32 || d == CLEF_F16; }
+
+}  // namespace
+}  // namespace clef
+
+using namespace clef;
+
+extern "C" int clef_rms_norm(const void* x, int64_t ldx, int dtype_in, const float* w, void* y,
+                             int64_t ldy, int dtype_out, int rows, int width, float eps,
+                             void* stream) {
+  if (ldx == 0) ldx = width;
+  if (ldy == 0) ldy = width;
+  CLEF_REQUIRE(x && w && y, "RMS: null pointer");
+  CLEF_REQUIRE(rows >= 1 && width >= 1 && ldx >= width && ldy >= width, "RMS: dimensions");
+  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "RMS: dtype");
+  CLEF_REQUIRE(eps > 0.0f && eps <= 1.0f, "RMS: epsilon");
+  hipLaunchKernelGGL(rms_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, x, ldx,
+                     dtype_in, w, y, ldy, dtype_out, rows, width, eps,
+                     static_cast<float>(1.0 / static_cast<double>(width)));
+  return check_launch("rms_norm");
+}
+
+extern "C" int clef_conv_silu(const void* x, int64_t ldx, int dtype_in, const float* history,
+                              int history_rows, const float* w, int taps, void* y, int64_t ldy,
+                              int dtype_out, int T, int W, void* stream) {
+  if (ldx == 0) ldx = W;
+  if (ldy == 0) ldy = W;
+  CLEF_REQUIRE(x && w && y, "conv: null pointer");
+  CLEF_REQUIRE(T >= 1 && W >= 1 && ldx >= W && ldy >= W, "conv: dimensions");
+  CLEF_REQUIRE(taps >= 1 && taps <= 8 && history_rows >= 0 && history_rows <= taps - 1 &&
+                   (history_rows == 0 || history),
+               "conv: taps or history");
+  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "conv: dtype");
+  const int64_t n = (int64_t)T * W;
+  hipLaunchKernelGGL(conv_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, ldx, dtype_in, history, history_rows, w, taps, y, ldy,
+                     dtype_out, T, W);
+  return check_launch("conv_silu");
+}
+
+extern "C" int clef_delta_gates(const void* a, int64_t lda, const void* b, int64_t ldb, int dtype_in,
+                                const float* dt, const float* a_log, float* g, float* beta, int T,
+                                int Hv, void* stream) {
+  if (lda == 0) lda = Hv;
+  if (ldb == 0) ldb = Hv;
+  CLEF_REQUIRE(a && b && dt && a_log && g && beta, "gates: null pointer");
+  CLEF_REQUIRE(T >= 1 && Hv >= 1 && lda >= Hv && ldb >= Hv, "gates: dimensions");
+  CLEF_REQUIRE(dtype_ok(dtype_in), "gates: dtype");
+  hipLaunchKernelGGL(gates_kernel, dim3((T * Hv + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                     a, lda, b, ldb, dtype_in, dt, a_log, g, beta, T, Hv);
+  return check_launch("delta_gates");
+}
+
+extern "C" int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, int dtype_z,
+                                   const float* w, void* y, int dtype_out, int T, int Hv, int width,
+                                   float eps, void* stream) {
+  if (ldz == 0) ldz = (int64_t)Hv * width;
+  CLEF_REQUIRE(o && z && w && y, "gated norm: null pointer");
+  CLEF_REQUIRE(T >= 1 && Hv >= 1 && width >= 1 && ldz >= (int64_t)Hv * width, "gated norm: dimensions");
+  CLEF_REQUIRE(dtype_ok(dtype_z) && dtype_ok(dtype_out), "gated norm: dtype");
+  hipLaunchKernelGGL(gated_rms_kernel, dim3((T * Hv + 3) / 4), dim3(256), 0, (hipStream_t)stream, o,
+                     z, ldz, dtype_z, w, y, dtype_out, T, Hv, width, eps,
+                     static_cast<float>(1.0 / static_cast<double>(width)));
+  return check_launch("gated_rms_silu");
+}
+
+extern "C" int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int dtype_in, const float* w,
+                                   void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
+                                   int rot_dim, double theta, int pos0, int dst_offset, float eps,
+                                   void* stream) {
+  if (hs == 0) hs = d;
+  if (ldx == 0) ldx = (int64_t)heads * hs;
+  CLEF_REQUIRE(x && w && y, "q/k norm: null pointer");
+  CLEF_REQUIRE(T >= 1 && heads >= 1 && d >= 1 && hs >= d && ldx >= (int64_t)(heads - 1) * hs + d,
+               "q/k norm: dimensions");
+  CLEF_REQUIRE(rot_dim >= 0 && rot_dim <= d && rot_dim % 2 == 0 && rot_dim / 2 <= 128,
+               "q/k norm: rotary width");
+  CLEF_REQUIRE(dst_offset >= 0 && ldy_tok >= (int64_t)dst_offset + T && pos0 >= 0, "q/k norm: destination");
+  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "q/k norm: dtype");
+  RotaryTable tab{};
+  for (int i = 0; i < rot_dim / 2; ++i)  // ops.rs:165: theta.powf(-(2i)/dim) in f64, then f32
+    tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
+  hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
+                     rot_dim, pos0, dst_offset, eps, static_cast<float>(1.0 / static_cast<double>(d)),
+                     tab);
+  return check_launch("qk_norm_rotary");
+}
+
+extern "C" int clef_values_transposed(const void* x, int64_t ldx, int dtype_in, void* y, int64_t ldy_tok,
+                                      int dtype_out, int T, int heads, int d, int dst_offset,
+                                      void* stream) {
+  if (ldx == 0) ldx = (int64_t)heads * d;
+  CLEF_REQUIRE(x && y, "values: null pointer");
+  CLEF_REQUIRE(T >= 1 && heads >= 1 && d >= 1 && ldx >= (int64_t)heads * d, "values: dimensions");
+  CLEF_REQUIRE(dst_offset >= 0 && ldy_tok >= (int64_t)dst_offset + T, "values: destination");
+  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "values: dtype");
+  hipLaunchKernelGGL(values_t_kernel, dim3((T + 63) / 64, (d + 63) / 64, heads), dim3(256), 0,
+                     (hipStream_t)stream, x, ldx, dtype_in, y, ldy_tok, dtype_out, T, heads, d, dst_offset);
+  return check_launch("values_transposed");
+}
+
+extern "C" int clef_embed(const int32_t* ids, int T, const void* table, int dtype, int vocab, int H,
+                          float* h, void* stream) {
+  CLEF_REQUIRE(ids && table && h, "embed: null pointer");
+  CLEF_REQUIRE(T >= 1 && vocab >= 1 && H >= 1 && dtype_ok(dtype), "embed: dimensions");
+  const int64_t n = (int64_t)T * H;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     ids, T, table, dtype, vocab, H, h);
+  return check_launch("embed");
+}
+
+extern "C" int clef_head_logits(const float* x, int H, const float* w, int n_logits, float* logits,
+                                void* stream) {
+  CLEF_REQUIRE(x && w && logits && H >= 1 && n_logits >= 1 && n_logits <= 65536, "head: arguments");
+  hipLaunchKernelGGL(head_kernel, dim3(n_logits), dim3(64), 0, (hipStream_t)stream, x, H, w, logits);
+  return check_launch("head_logits");
+}

@@ -125,10 +125,12 @@ int clef_delta_gates(const void* a, int64_t lda, const void* b, int64_t ldb, int
                      const float* dt, const float* a_log, float* g, float* beta, int T, int Hv,
                      void* stream);
 /*
- * Gated output norm: y = round(rms_w(o)) * silu(z), rows of `width` (one row
- * per token and v-head), qwen.rs:671-676.  o: [rows, width] f32; z: (stride
- * ldz per token row of Hv*width, dtype_z); y [rows, width] dtype_out.
- * `round_dtype` is the dtype the reference casts the norm output to first.
+ * Gated output norm, qwen.rs:671-676: per token and v-head row of `width`,
+ * o is rounded to dtype_out (the scan output cast to the activation dtype),
+ * RMS-normalised in f32 with w (no offset), rounded to dtype_out, multiplied
+ * by silu(z) in f32 and rounded to dtype_out.  o: [T, Hv, width] f32
+ * contiguous; z: [T, Hv, width] with token stride ldz (dtype_z); y: [T,
+ * Hv*width] contiguous.
  */
 int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, int dtype_z, const float* w,
                         void* y, int dtype_out, int T, int Hv, int width, float eps,
@@ -138,29 +140,43 @@ int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, int dtype_z,
 /* Gated full-attention layer pieces (qwen.rs:451-525; ops.rs:62-188)      */
 /* ---------------------------------------------------------------------- */
 /*
- * Per-head RMSNorm (offset weights, eps) then rotary (rotate-half, angle
- * (pos0 + t) * theta^(-2i/rot_dim) on the first rot_dim features), writing
- * head-major [H, T_total, d] at token offset `dst_offset` (so cached prefix
- * keys may precede it).  x: token stride ldx, head stride d.
+ * Per-head RMSNorm then rotary, for the attention q and k (qwen.rs:437-470;
+ * ops.rs:17-32, 150-185).  x: [T, heads, *] with token stride ldx and head
+ * stride hs (the q projection interleaves [q | gate] per head, so hs = 2d);
+ * w: [d] f32 norm weights, already offset (1 + w).  The norm output is
+ * rounded to dtype_out, rotated on the first rot_dim features (rotate-half;
+ * angle (pos0 + t) * theta^(-2i/rot_dim), the exponent taken in f64) and
+ * rounded again.  y is head-major [heads, ldy_tok, d]: row (h, dst_offset + t).
  */
-int clef_qk_norm_rotary(const void* x, int64_t ldx, int dtype_in, const float* w, void* y,
-                        int dtype_out, int T, int heads, int d, int rot_dim, double theta,
-                        int pos0, int dst_offset, int dst_tokens, float eps, void* stream);
-/* Head-major copy of values: x [T, heads, d] (token stride ldx) -> y [heads, dst_tokens, d]. */
-int clef_head_major(const void* x, int64_t ldx, int dtype_in, void* y, int dtype_out, int T,
-                    int heads, int d, int dst_offset, int dst_tokens, void* stream);
+int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int dtype_in, const float* w,
+                        void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
+                        int rot_dim, double theta, int pos0, int dst_offset, float eps,
+                        void* stream);
+/*
+ * Value layout for attention: x [T, heads, d] (token stride ldx, head stride
+ * d) -> y transposed per head, [heads, d, ldy_tok] with token (dst_offset + t)
+ * contiguous, so that P.V reads 16-byte runs of consecutive keys.
+ */
+int clef_values_transposed(const void* x, int64_t ldx, int dtype_in, void* y, int64_t ldy_tok,
+                           int dtype_out, int T, int heads, int d, int dst_offset, void* stream);
 /*
  * Causal GQA attention with online softmax (bottom-right aligned mask when
- * kn > qn), output gated by sigmoid(gate):
- *   y[t, h*d + e] = attn(q,k,v)[h, t, e] * sigmoid(gate[t, h*d + e]).
- * Replaces ops::attention + the sigmoid gate (qwen.rs:511-524) and the
- * "clef-f32-flash-attention" op (metal.rs:528-633).  q [H, qn, d];
- * k, v [KVH, kn, d]; gate token stride ldg.  dtype: operand dtype of q/k/v
- * (f16: f16 MFMA, f32: f32 MFMA), accumulation f32.  d in {64, 128, 256}.
+ * kn > qn) and sigmoid output gate:
+ *   y[t, h*d + e] = attn(q,k,v)[h, t, e] * sigmoid(gate[t, h, e])
+ * Replaces ops::attention + the gate of qwen.rs:511-524 and the
+ * "clef-f32-flash-attention" op (metal.rs:528-633).
+ * q [heads, ldq_tok, d] (rows 0..qn-1), k [kv_heads, ldk_tok, d],
+ * vt [kv_heads, d, ldv_tok] (from clef_values_transposed); gate token stride
+ * ldg and head stride hsg; y [qn, heads*d] token stride ldy.  dtype is the
+ * operand dtype of q/k/v/gate (f16: f16 MFMA, f32: f32 MFMA), accumulation
+ * and softmax in f32; y in dtype (the product of the rounded attention and
+ * the rounded gate, as the reference's mixed profile does).  d in {64, 128,
+ * 256}; heads % kv_heads == 0; qn <= kn.
  */
-int clef_attention_gated(const void* q, const void* k, const void* v, int dtype, int heads,
-                         int kv_heads, int qn, int kn, int d, const void* gate, int64_t ldg,
-                         void* y, int64_t ldy, int dtype_out, void* stream);
+int clef_attention_gated(const void* q, int64_t ldq_tok, const void* k, int64_t ldk_tok,
+                         const void* vt, int64_t ldv_tok, int dtype, int heads, int kv_heads,
+                         int qn, int kn, int d, const void* gate, int64_t ldg, int64_t hsg,
+                         void* y, int64_t ldy, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Embedding gather and pooled head                                         */
@@ -171,6 +187,72 @@ int clef_embed(const int32_t* ids, int T, const void* table, int dtype, int voca
 /* logits[j] = sum_k x[row, k] * W[j, k], f32 (last-token pooled head). */
 int clef_head_logits(const float* x, int H, const float* w, int n_logits, float* logits,
                      void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Hybrid backbone prefill (host orchestration over the kernels above)     */
+/* ---------------------------------------------------------------------- */
+/*
+ * Replaces Backbone::{load, prefill, forward} (crates/core/src/models/qwen.rs:
+ * 193-426) with the DeltaNet mixer Delta::forward (:589-688) and the gated
+ * attention layer FullAttention::forward (:451-525).  Layer kinds: 0 =
+ * linear_attention (DeltaNet), 1 = full_attention.
+ *
+ * Profiles: CLEF_PROFILE_F32 runs every projection on f32 MFMA and the strict
+ * scan (the reference's CPU/Metal F32 profile); CLEF_PROFILE_MIXED_F16 runs
+ * f16 projections with f32 accumulation and the reference's half rounding
+ * points, an f32 residual stream, and the scan in `scan_precision`.
+ */
+enum { CLEF_PROFILE_F32 = 0, CLEF_PROFILE_MIXED_F16 = 1 };
+
+typedef struct {
+    int hidden, intermediate, vocab;
+    int heads, kv_heads, head_dim, rotary_dim;
+    int lin_k_heads, lin_v_heads, lin_dk, lin_dv, conv_taps;
+    int n_layers;
+    float eps;
+    double rope_theta;
+    int profile;        /* CLEF_PROFILE_* */
+    int scan_precision; /* CLEF_SCAN_* */
+    int max_tokens;     /* prefix + new tokens per prefill (reference: 4096) */
+} clef_backbone_config;
+
+/* Device pointers to one layer's checkpoint tensors.  Matrices ([out, in],
+ * row-major) are in the profile dtype (f16 for MIXED_F16, f32 for F32);
+ * vectors and the conv kernel are f32 and raw (the (1+w) norm offsets are
+ * applied at create, normalization.rs:37-46).  Unused fields may be NULL. */
+typedef struct {
+    int kind;
+    const void *input_norm, *post_norm;          /* [H] f32 */
+    const void *gate, *up, *down;                /* [I,H], [I,H], [H,I] */
+    const void *qkv, *z, *a, *b, *out;           /* DeltaNet projections */
+    const void *conv, *dt, *a_log, *norm;        /* [W,taps], [Hv], [Hv], [dv] f32 */
+    const void *q, *k, *v, *o;                   /* attention projections */
+    const void *q_norm, *k_norm;                 /* [d] f32 */
+} clef_layer_weights;
+
+typedef struct clef_backbone clef_backbone;
+
+/* Copies what it must (fused in-projections, offset norms) into memory the
+ * backbone owns until clef_backbone_destroy; the MLP and output matrices and
+ * the embedding table are referenced in place and must outlive it. */
+int clef_backbone_create(const clef_backbone_config* config, const clef_layer_weights* layers,
+                         const void* embeddings, const void* final_norm, clef_backbone** out);
+void clef_backbone_destroy(clef_backbone* b);
+/* Workspace for a prefill of T new tokens after `prefix_tokens` cached ones. */
+size_t clef_backbone_workspace(const clef_backbone* b, int T, int prefix_tokens);
+/* Bytes of a prefix state (PrefixState, qwen.rs:153-191) at `tokens`. */
+size_t clef_backbone_prefix_bytes(const clef_backbone* b, int tokens);
+/*
+ * ids: host int32 [T], each < vocab.  initial: a prefix state buffer written
+ * by an earlier capture (initial_tokens of them), or NULL.  capture in 1..T-1
+ * writes the state after `capture` tokens into `saved` (which must hold
+ * clef_backbone_prefix_bytes(b, capture) bytes); initial and capture are
+ * exclusive (qwen.rs:345-359).  hidden: f32 [(initial_tokens + T), H], the
+ * final-normed hidden states, prefix rows included.
+ */
+int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T, const void* initial,
+                          int initial_tokens, int capture, void* saved, float* hidden,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,136 @@
+"""Hybrid backbone prefill on the GPU against the reference's golden fixture
+and the CPU oracle.
+
+Bars: the f32 profile must reproduce the reference's golden hidden states of
+the synthetic backbone fixture within the reference's own tolerance
+(1e-5 + 1e-4|e|, mod.rs:75-111) and the oracle within the same bar; the
+mixed-f16 profile must stay within rtol 2e-2 of the F32 path (elementwise,
+with an absolute floor of 2e-2 * max|e| for near-zero entries) and give the
+same argmax decision.
+"""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+gpu = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def clef():
+    import clef_hip
+    clef_hip.lib()
+    return clef_hip
+
+
+@pytest.fixture(scope="module")
+def fixture(golden_dir):
+    from safetensors.numpy import load_file
+    cfg = json.loads((golden_dir / "backbone-config.json").read_text())
+    w = load_file(str(golden_dir / "backbone.safetensors"))
+    exp = load_file(str(golden_dir / "backbone-output.safetensors"))["hidden"]
+    return cfg, w, exp
+
+
+def _close(actual, expected, atol, rtol):
+    actual, expected = np.asarray(actual, np.float64), np.asarray(expected, np.float64)
+    assert np.isfinite(actual).all()
+    err = np.abs(actual - expected)
+    bad = err > atol + rtol * np.abs(expected)
+    assert not bad.any(), f"{bad.sum()}/{bad.size} out of tolerance, max err {err.max():.3e}"
+
+
+def _mixed_close(actual, expected):
+    expected = np.asarray(expected, np.float64)
+    _close(actual, expected, 2e-2 * np.abs(expected).max(), 2e-2)
+
+
+def _to_dev(w):
+    return {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in w.items()}
+
+
+@gpu
+def test_fixture_backbone_f32_matches_reference_golden(clef, fixture):
+    cfg, w, exp = fixture
+    b = clef.Backbone(cfg, _to_dev(w), profile="f32")
+    hidden, _ = b.prefill(np.arange(20))
+    _close(hidden.cpu().numpy(), exp, 1e-5, 1e-4)
+    ref, _ = oracle.Backbone(cfg, w).prefill(np.arange(20))
+    _close(hidden.cpu().numpy(), ref, 1e-5, 1e-4)
+
+
+@gpu
+@pytest.mark.parametrize("scan", ["mixed", "strict"])
+def test_fixture_backbone_mixed_profile(clef, fixture, scan):
+    cfg, w, exp = fixture
+    b = clef.Backbone(cfg, _to_dev(w), profile="mixed", scan_precision=scan)
+    hidden, _ = b.prefill(np.arange(20))
+    _mixed_close(hidden.cpu().numpy(), exp)
+    emul, _ = oracle.Backbone(cfg, w, mixed_f16=True).prefill(np.arange(20))
+    _close(hidden.cpu().numpy(), emul, 5e-3, 5e-3)
+
+
+@gpu
+@pytest.mark.parametrize("profile", ["f32", "mixed"])
+def test_fixture_prefix_capture_and_resume(clef, fixture, profile):
+    """mod.rs:113-171 on the device path."""
+    cfg, w, _ = fixture
+    b = clef.Backbone(cfg, _to_dev(w), profile=profile)
+    ids = np.arange(20)
+    expected = b.prefill(ids)[0].cpu().numpy()
+    check = (lambda a, e: _close(a, e, 1e-5, 1e-4)) if profile == "f32" else \
+        (lambda a, e: _close(a, e, 2e-3, 2e-3))
+    for boundary in (1, 2, 3, 8, 19):
+        captured, state = b.prefill(ids, capture=boundary)
+        assert np.array_equal(captured.cpu().numpy(), expected)  # capturing changes nothing
+        with pytest.raises(clef.ClefError):
+            b.prefill(ids[boundary:], initial=state, capture=1)
+        resumed, _ = b.prefill(ids[boundary:], initial=state)
+        check(resumed.cpu().numpy(), expected)
+        changed = ids.copy()
+        changed[boundary:] += 20
+        resumed, _ = b.prefill(changed[boundary:], initial=state)
+        check(resumed.cpu().numpy(), b.prefill(changed)[0].cpu().numpy())
+        again, _ = b.prefill(ids[boundary:], initial=state)  # the state is not mutated
+        check(again.cpu().numpy(), expected)
+    with pytest.raises(clef.ClefError):
+        b.prefill(ids, capture=20)
+    with pytest.raises(clef.ClefError):
+        b.prefill(np.array([64]))
+
+
+@pytest.fixture(scope="module")
+def block_case():
+    import workloads
+    cfg = workloads.block_config()
+    w = workloads.block_weights(cfg, seed=3)
+    ids = workloads.block_ids(cfg, 2048, seed=3).numpy()
+    head = workloads.block_head(cfg, seed=3)
+    # the oracle needs only the gathered embedding rows: remap ids onto them
+    uniq, inv = np.unique(ids, return_inverse=True)
+    wh = {k: v.cpu().numpy() for k, v in w.items() if k != "model.language_model.embed_tokens.weight"}
+    emb = w["model.language_model.embed_tokens.weight"]
+    wh["model.language_model.embed_tokens.weight"] = emb[torch.from_numpy(uniq).long().cuda()].cpu().numpy()
+    cfg_small = dict(cfg, vocab_size=len(uniq))
+    ref, _ = oracle.Backbone(cfg_small, wh).prefill(inv.astype(np.int32))
+    ref_logits = ref[-1].astype(np.float64) @ head.cpu().numpy().astype(np.float64).T
+    return cfg, w, ids, head, ref, ref_logits
+
+
+@gpu
+@pytest.mark.parametrize("profile", ["f32", "mixed"])
+def test_block_prefill_matches_oracle(clef, block_case, profile):
+    """3 DeltaNet + 1 gated attention layer, hidden 2048, T = 2048, seed 3."""
+    cfg, w, ids, head, ref, ref_logits = block_case
+    b = clef.Backbone(cfg, w, profile=profile)
+    hidden, _ = b.prefill(ids)
+    logits = clef.head_logits(hidden[-1], head).cpu().numpy()
+    got = hidden.cpu().numpy()
+    if profile == "f32":
+        _close(got, ref, 1e-4, 1e-4)
+    else:
+        _mixed_close(got, ref)
+    assert int(np.argmax(logits)) == int(np.argmax(ref_logits))

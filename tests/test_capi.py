@@ -1,0 +1,84 @@
+"""The C-ABI library loads and exports every entry point include/clef_hip.h
+declares, and rejects invalid requests before touching the device.  No
+kernel is launched here (these tests run without a GPU)."""
+import ctypes as C
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "clef_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(clef_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def clef():
+    import clef_hip
+    clef_hip.lib()
+    return clef_hip
+
+
+def test_library_exports_every_declared_symbol(clef):
+    names = declared_functions()
+    assert len(names) >= 20
+    lib = C.CDLL(str(clef.LIB_PATH))
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(clef.SIGNATURES), set(names) ^ set(clef.SIGNATURES)
+
+
+def test_abi_version(clef):
+    assert clef.lib().clef_hip_abi_version() == 1
+
+
+@pytest.mark.parametrize("shape", [(0, 32, 32, 128, 128), (4097 * 256, 16, 32, 128, 128),
+                                   (1, 2, 3, 128, 128), (1, 1, 1, 129, 128), (1, 1, 1, 128, 129),
+                                   (1, 1, 1, 0, 4)])
+def test_scan_rejects_unsupported_shapes_before_launch(clef, shape):
+    """metal.rs:945-956: dimension checks happen before any allocation."""
+    T, Hk, Hv, dk, dv = shape
+    assert clef.lib().clef_delta_scan_workspace(T, Hk, Hv, dk, dv, 64, 0) == 0
+    rc = clef.lib().clef_delta_scan(1, 1, 1, 0, 0, 0, 1, 1, 0, 0, T, Hk, Hv, dk, dv, 64, 0, None, 0,
+                                    1, 0, 0, None, None, 1, 1 << 30, None)
+    assert rc < 0
+    assert "DeltaNet scan" in clef.last_error()
+
+
+def test_scan_rejects_bad_chunk_capture_and_workspace(clef):
+    L = clef.lib()
+    assert L.clef_delta_scan_workspace(256, 4, 4, 64, 64, 32, 0) == 0
+    ws = L.clef_delta_scan_workspace(256, 4, 4, 64, 64, 64, 0)
+    assert ws > 0
+    args = lambda capture, wsb: (1, 1, 1, 0, 0, 0, 1, 1, 0, 0, 256, 4, 4, 64, 64, 64, 0, None,
+                                 capture, 1, 0, 0, None, None, 256, wsb, None)
+    assert L.clef_delta_scan(*args(300, ws)) < 0          # capture beyond T
+    assert L.clef_delta_scan(*args(5, ws)) < 0            # capture without a buffer
+    assert L.clef_delta_scan(*args(0, ws - 1)) < 0        # workspace too small
+    assert "workspace" in clef.last_error()
+
+
+def test_gemm_and_pointwise_validation(clef):
+    L = clef.lib()
+    assert L.clef_gemm(None, 0, 1, 0, 1, 0, 4, 4, 4, 1, 1, 0, None) < 0
+    assert L.clef_gemm(1, 0, 1, 0, 1, 0, 0, 4, 4, 1, 1, 0, None) < 0
+    assert L.clef_gemm(1, 2, 1, 0, 1, 0, 4, 4, 4, 1, 1, 0, None) < 0   # ldx < K
+    assert L.clef_gemm(1, 0, 1, 0, 1, 0, 4, 4, 4, 7, 1, 0, None) < 0   # dtype
+    assert L.clef_rms_norm(1, 0, 0, 1, 1, 0, 0, 4, 8, 0.0, None) < 0   # eps
+    assert L.clef_conv_silu(1, 0, 0, None, 2, 1, 4, 1, 0, 0, 4, 8, None) < 0  # history rows w/o data
+    assert L.clef_attention_gated(1, 64, 1, 64, 1, 64, 1, 3, 2, 4, 4, 64, 1, 128, 128, 1, 192, None) < 0
+    assert L.clef_attention_gated(1, 64, 1, 64, 1, 64, 1, 4, 2, 8, 4, 64, 1, 128, 128, 1, 256, None) < 0
+
+
+def test_backbone_create_rejects_bad_config(clef):
+    cfg = clef.BackboneConfig()
+    cfg.hidden, cfg.intermediate, cfg.vocab, cfg.n_layers = 16, 32, 64, 1
+    cfg.eps, cfg.profile, cfg.max_tokens = 0.0, 0, 4096
+    layers = (clef.LayerWeights * 1)()
+    handle = C.c_void_p()
+    assert clef.lib().clef_backbone_create(C.byref(cfg), layers, 1, 1, C.byref(handle)) < 0
+    assert not handle.value
