@@ -311,7 +311,12 @@ SIGNATURES.update({
     "clef_backbone_workspace": (_z, [_p, _i, _i]),
     "clef_backbone_prefix_bytes": (_z, [_p, _i]),
     "clef_backbone_prefill": (_i, [_p, C.POINTER(C.c_int32), _i, _p, _i, _i, _p, _p, _p, _z, _p]),
+    "clef_backbone_enable_timing": (_i, [_p, _i]),
+    "clef_backbone_timings": (_i, [_p, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double),
+                                   C.POINTER(C.c_double)]),
 })
+
+CATEGORIES = ("gemm", "scan", "attention", "conv", "norm", "other")
 
 
 class PrefixState:
@@ -413,6 +418,18 @@ class Backbone:
         if self._ws is None or self._ws.numel() < n:
             self._ws = torch.empty(n, dtype=torch.uint8, device=device)
         return self._ws
+
+    def enable_timing(self, enable=True):
+        _check(lib().clef_backbone_enable_timing(self._h, int(enable)))
+
+    def timings(self):
+        """Per-category {ms, launches, flops, bytes} of the prefills since the last call."""
+        n = len(CATEGORIES)
+        ms, cnt = (C.c_double * n)(), (C.c_int * n)()
+        fl, by = (C.c_double * n)(), (C.c_double * n)()
+        _check(lib().clef_backbone_timings(self._h, ms, cnt, fl, by))
+        return {name: {"ms": ms[i], "launches": cnt[i], "flops": fl[i], "bytes": by[i]}
+                for i, name in enumerate(CATEGORIES)}
 
     def prefix_bytes(self, tokens):
         return lib().clef_backbone_prefix_bytes(self._h, tokens)

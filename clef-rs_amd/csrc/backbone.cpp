@@ -57,8 +57,17 @@ struct LayerState {
 
 }  // namespace clef
 
+struct TimingRecord {
+  int cat;
+  hipEvent_t start, stop;
+  double flops, bytes;
+};
+
 struct clef_backbone {
   clef_backbone_config c;
+  bool timing = false;
+  std::vector<TimingRecord> records;
+  std::vector<hipEvent_t> event_pool;
   std::vector<clef::LayerState> layers;
   const void* embeddings = nullptr;
   float* final_norm = nullptr;
@@ -74,6 +83,17 @@ namespace {
 int hip_fail(hipError_t e, const char* what) {
   return fail(static_cast<int>(e), std::string(what) + ": " + hipGetErrorString(e));
 }
+
+#define CLEF_TRY(expr)        \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_ != 0) return rc_; \
+  } while (0)
+#define HIP_TRY(expr, what)                          \
+  do {                                               \
+    hipError_t e_ = (expr);                          \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
 
 struct Workspace {
   int32_t* ids;
@@ -166,16 +186,30 @@ size_t prefix_layout(const clef_backbone* b, int tokens, char* base, PrefixView*
   return off;
 }
 
-#define CLEF_TRY(expr)        \
-  do {                        \
-    int rc_ = (expr);         \
-    if (rc_ != 0) return rc_; \
-  } while (0)
-#define HIP_TRY(expr, what)                          \
-  do {                                               \
-    hipError_t e_ = (expr);                          \
-    if (e_ != hipSuccess) return hip_fail(e_, what); \
-  } while (0)
+
+hipEvent_t pooled_event(clef_backbone* b) {
+  if (!b->event_pool.empty()) {
+    hipEvent_t e = b->event_pool.back();
+    b->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Runs `launch` and, while timing is enabled, brackets it with an event pair.
+template <class F>
+int timed(clef_backbone* b, int cat, double flops, double bytes, hipStream_t s, F&& launch) {
+  if (!b->timing) return launch();
+  TimingRecord r{cat, pooled_event(b), pooled_event(b), flops, bytes};
+  if (!r.start || !r.stop) return fail(-2, "timing: event creation failed");
+  HIP_TRY(hipEventRecord(r.start, s), "timing event");
+  const int rc = launch();
+  HIP_TRY(hipEventRecord(r.stop, s), "timing event");
+  b->records.push_back(r);
+  return rc;
+}
 
 int copy_rows(void* dst, const void* src, size_t bytes, hipStream_t s) {
   if (bytes == 0) return 0;
@@ -308,8 +342,39 @@ extern "C" int clef_backbone_create(const clef_backbone_config* config, const cl
 
 extern "C" void clef_backbone_destroy(clef_backbone* b) {
   if (!b) return;
+  for (auto& r : b->records) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  for (hipEvent_t e : b->event_pool) (void)hipEventDestroy(e);
   for (void* p : b->owned) (void)hipFree(p);
   delete b;
+}
+
+extern "C" int clef_backbone_enable_timing(clef_backbone* b, int enable) {
+  CLEF_REQUIRE(b, "timing: null backbone");
+  b->timing = enable != 0;
+  return 0;
+}
+
+extern "C" int clef_backbone_timings(clef_backbone* b, double* ms, int* launches, double* flops, double* bytes) {
+  CLEF_REQUIRE(b && ms && launches && flops && bytes, "timing: null argument");
+  for (int i = 0; i < CLEF_CAT_COUNT; ++i) ms[i] = flops[i] = bytes[i] = 0.0, launches[i] = 0;
+  int rc = 0;
+  for (auto& r : b->records) {
+    float t = 0.0f;
+    hipError_t e = hipEventSynchronize(r.stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, r.start, r.stop);
+    if (e != hipSuccess && rc == 0) rc = fail(static_cast<int>(e), "timing: event query failed");
+    ms[r.cat] += t;
+    launches[r.cat] += 1;
+    flops[r.cat] += r.flops;
+    bytes[r.cat] += r.bytes;
+    b->event_pool.push_back(r.start);
+    b->event_pool.push_back(r.stop);
+  }
+  b->records.clear();
+  return rc;
 }
 
 extern "C" size_t clef_backbone_workspace(const clef_backbone* b, int T, int prefix_tokens) {
@@ -350,32 +415,52 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
   const size_t a = elt(ad);
   float* h = hidden + (size_t)offset * H;  // residual stream of the new tokens
   HIP_TRY(hipMemcpyAsync(w.ids, ids, sizeof(int32_t) * T, hipMemcpyHostToDevice, s), "ids upload");
-  CLEF_TRY(clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
+#define TIMED(cat, flops, bytes, expr) \
+  CLEF_TRY(timed(b, cat, static_cast<double>(flops), static_cast<double>(bytes), s, [&]() { return (expr); }))
+  const double da = static_cast<double>(a);
+  auto gemm_bytes = [&](double M, double N, double K, bool residual) {
+    return da * (M * K + N * K) + (residual ? 8.0 * M * N : da * M * N);
+  };
+  TIMED(CLEF_CAT_OTHER, 0, (4.0 + da) * T * H, clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
   const int Hv = c.lin_v_heads, dv = c.lin_dv, taps = c.conv_taps;
   const int heads = c.heads, kvh = c.kv_heads, d = c.head_dim;
   const int Ttot = offset + T;
+  const double rms_bytes = (4.0 + da) * T * H;
 
   for (int li = 0; li < c.n_layers; ++li) {
     const LayerState& L = b->layers[li];
-    CLEF_TRY(clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
+    TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
       char* proj = static_cast<char*>(w.proj);
-      CLEF_TRY(clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NP, H, ad, ad, CLEF_EPI_STORE, s));
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * NP * H, gemm_bytes(T, NP, H, false),
+            clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NP, H, ad, ad, CLEF_EPI_STORE, s));
       const int hist_rows = initial ? (offset < taps - 1 ? offset : taps - 1) : 0;
-      CLEF_TRY(clef_conv_silu(proj, NP, ad, initial ? init.hist[li] : nullptr, hist_rows, L.conv, taps, w.mixed,
-                              Wc, b->conv_dt, T, Wc, s));
-      CLEF_TRY(clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt,
-                                L.a_log, w.g, w.beta, T, Hv, s));
+      const double ce = static_cast<double>(elt(b->conv_dt));
+      TIMED(CLEF_CAT_CONV, 2.0 * T * Wc * taps, (da + ce) * T * Wc,
+            clef_conv_silu(proj, NP, ad, initial ? init.hist[li] : nullptr, hist_rows, L.conv, taps, w.mixed, Wc,
+                           b->conv_dt, T, Wc, s));
+      TIMED(CLEF_CAT_OTHER, 0, (2.0 * da + 8.0) * T * Hv,
+            clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt, L.a_log,
+                             w.g, w.beta, T, Hv, s));
       const char* mixed = static_cast<const char*>(w.mixed);
-      const size_t ce = elt(b->conv_dt);
-      CLEF_TRY(clef_delta_scan(mixed, mixed + ce * b->key, mixed + ce * 2 * b->key, Wc, Wc, b->conv_dt, w.g,
-                               w.beta, Hv, CLEF_F32, T, c.lin_k_heads, Hv, c.lin_dk, dv, 64, c.scan_precision,
-                               initial ? init.rec[li] : nullptr, capture, w.scan_out, (int64_t)Hv * dv,
-                               CLEF_F32, capture ? sav.rec[li] : nullptr, nullptr, w.scan_ws,
-                               w.scan_ws_bytes, s));
-      CLEF_TRY(clef_gated_rms_silu(w.scan_out, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
-      CLEF_TRY(clef_gemm(w.gated, b->value, L.out, b->value, h, H, T, H, b->value, ad, ad, CLEF_EPI_RESIDUAL, s));
+      const size_t ces = elt(b->conv_dt);
+      const double nchunk = (T + 63) / 64;
+      const double scan_flops =
+          nchunk * (c.lin_k_heads * 4.0 * 64 * 64 * c.lin_dk +
+                    Hv * (2.0 * 64 * 64 * c.lin_dk + 4.0 * 64 * 64 * dv + 6.0 * 64 * c.lin_dk * dv + 64.0 * 64 * 64 * 2 / 3));
+      const double state = 4.0 * Hv * c.lin_dk * dv;
+      const double scan_bytes = ce * T * (2.0 * b->key + b->value) + 8.0 * T * Hv + 4.0 * T * b->value +
+                                (initial ? state : 0.0) + (capture ? state : 0.0);
+      TIMED(CLEF_CAT_SCAN, scan_flops, scan_bytes,
+            clef_delta_scan(mixed, mixed + ces * b->key, mixed + ces * 2 * b->key, Wc, Wc, b->conv_dt, w.g, w.beta, Hv,
+                            CLEF_F32, T, c.lin_k_heads, Hv, c.lin_dk, dv, 64, c.scan_precision,
+                            initial ? init.rec[li] : nullptr, capture, w.scan_out, (int64_t)Hv * dv, CLEF_F32,
+                            capture ? sav.rec[li] : nullptr, nullptr, w.scan_ws, w.scan_ws_bytes, s));
+      TIMED(CLEF_CAT_NORM, 6.0 * T * b->value, (4.0 + 2.0 * da) * T * b->value,
+            clef_gated_rms_silu(w.scan_out, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * H * b->value, gemm_bytes(T, H, b->value, true),
+            clef_gemm(w.gated, b->value, L.out, b->value, h, H, T, H, b->value, ad, ad, CLEF_EPI_RESIDUAL, s));
       if (capture) {  // conv history: last min(capture, taps-1) projected rows (qwen.rs:677-685)
         const int count = capture < taps - 1 ? capture : taps - 1;
         if (count > 0) {
@@ -387,10 +472,12 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
     } else {
       const int NA = b->NA;
       char* proj = static_cast<char*>(w.proj);
-      CLEF_TRY(clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * NA * H, gemm_bytes(T, NA, H, false),
+            clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
       const size_t koff = a * 2 * heads * d, voff = koff + a * kvh * d;
-      CLEF_TRY(clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
-                                   c.rope_theta, offset, 0, c.eps, s));
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
+            clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim, c.rope_theta,
+                                offset, 0, c.eps, s));
       if (initial) {  // cached keys and values precede the new ones (qwen.rs:486-496)
         for (int g = 0; g < kvh; ++g)
           CLEF_TRY(copy_rows(static_cast<char*>(w.kh) + a * (size_t)g * Ttot * d,
@@ -399,9 +486,11 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
                                  hipMemcpyDeviceToDevice, s),
                 "value prefix copy");
       }
-      CLEF_TRY(clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
-                                   c.rope_theta, offset, offset, c.eps, s));
-      CLEF_TRY(clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, offset, s));
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
+            clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
+                                c.rope_theta, offset, offset, c.eps, s));
+      TIMED(CLEF_CAT_OTHER, 0, 2.0 * da * T * kvh * d,
+            clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, offset, s));
       if (capture) {
         for (int g = 0; g < kvh; ++g)
           CLEF_TRY(copy_rows(static_cast<char*>(sav.key[li]) + a * (size_t)g * capture * d,
@@ -410,16 +499,23 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
                                  hipMemcpyDeviceToDevice, s),
                 "value capture");
       }
-      CLEF_TRY(clef_attention_gated(w.qh, T, w.kh, Ttot, w.vt, w.ldv, ad, heads, kvh, T, Ttot, d, proj + a * d,
-                                    NA, 2 * d, w.gated, (int64_t)heads * d, s));
-      CLEF_TRY(clef_gemm(w.gated, heads * d, L.out, heads * d, h, H, T, H, heads * d, ad, ad, CLEF_EPI_RESIDUAL, s));
+      const double pairs = static_cast<double>(T) * offset + 0.5 * T * (T + 1.0);
+      TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pairs, da * (3.0 * T * heads * d + 2.0 * Ttot * kvh * d),
+            clef_attention_gated(w.qh, T, w.kh, Ttot, w.vt, w.ldv, ad, heads, kvh, T, Ttot, d, proj + a * d, NA,
+                                 2 * d, w.gated, (int64_t)heads * d, s));
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * H * heads * d, gemm_bytes(T, H, heads * d, true),
+            clef_gemm(w.gated, heads * d, L.out, heads * d, h, H, T, H, heads * d, ad, ad, CLEF_EPI_RESIDUAL, s));
     }
-    CLEF_TRY(clef_rms_norm(h, H, CLEF_F32, L.post_norm, w.n, H, ad, T, H, c.eps, s));
-    CLEF_TRY(clef_gemm_swiglu(w.n, H, L.gate, L.up, H, w.mlp, c.intermediate, T, c.intermediate, H, ad, s));
-    CLEF_TRY(clef_gemm(w.mlp, c.intermediate, L.down, c.intermediate, h, H, T, H, c.intermediate, ad, ad,
-                       CLEF_EPI_RESIDUAL, s));
+    TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.post_norm, w.n, H, ad, T, H, c.eps, s));
+    const double I = c.intermediate;
+    TIMED(CLEF_CAT_GEMM, 4.0 * T * I * H, da * (T * H + 2.0 * I * H + T * I),
+          clef_gemm_swiglu(w.n, H, L.gate, L.up, H, w.mlp, c.intermediate, T, c.intermediate, H, ad, s));
+    TIMED(CLEF_CAT_GEMM, 2.0 * T * I * H, gemm_bytes(T, H, I, true),
+          clef_gemm(w.mlp, c.intermediate, L.down, c.intermediate, h, H, T, H, c.intermediate, ad, ad,
+                    CLEF_EPI_RESIDUAL, s));
   }
-  CLEF_TRY(clef_rms_norm(h, H, CLEF_F32, b->final_norm, h, H, CLEF_F32, T, H, c.eps, s));
+  TIMED(CLEF_CAT_NORM, 4.0 * T * H, 8.0 * T * H, clef_rms_norm(h, H, CLEF_F32, b->final_norm, h, H, CLEF_F32, T, H, c.eps, s));
+#undef TIMED
   if (initial) CLEF_TRY(copy_rows(hidden, init.hidden, 4ull * offset * H, s));
   if (capture) CLEF_TRY(copy_rows(sav.hidden, h, 4ull * capture * H, s));
   return 0;

@@ -254,6 +254,20 @@ int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T, const voi
                           int initial_tokens, int capture, void* saved, float* hidden,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Diagnostics, the counterpart of the reference's test-only `measured!`
+ * categories (crates/core/src/models/mod.rs:3-14, diagnostics.rs:43-96):
+ * while enabled, prefills record a hipEvent pair on the stream around every
+ * launch, by category.  clef_backbone_timings waits for those events, returns
+ * per-category totals (milliseconds, launch counts, algorithmic flops and
+ * algorithmic HBM bytes) and clears them.
+ */
+enum { CLEF_CAT_GEMM = 0, CLEF_CAT_SCAN, CLEF_CAT_ATTENTION, CLEF_CAT_CONV, CLEF_CAT_NORM,
+       CLEF_CAT_OTHER, CLEF_CAT_COUNT };
+int clef_backbone_enable_timing(clef_backbone* b, int enable);
+int clef_backbone_timings(clef_backbone* b, double* ms, int* launches, double* flops,
+                          double* bytes);
+
 #ifdef __cplusplus
 }
 #endif
