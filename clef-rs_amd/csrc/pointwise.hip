@@ -72,6 +72,163 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const void* x, int64_t l
   st(y, (int64_t)t * ldy + c, dto, acc / (1.0f + expf(-acc)));
 }
 
+// Vectorised conv + SiLU: 8 consecutive channels per thread and a run of
+// kConvRun tokens, with the 3-row history window kept in registers (taps <= 4).
+constexpr int kConvRun = 16;
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void conv_silu_vec_kernel(const TI* __restrict__ x, int64_t ldx,
+                                                            const float* __restrict__ hist, int hrows,
+                                                            const float* __restrict__ w, int taps,
+                                                            TO* __restrict__ y, int64_t ldy, int T, int W) {
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c0 >= W) return;
+  const int t0 = blockIdx.y * kConvRun;
+  float wt[8][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wt[j][k] = k < taps ? w[(int64_t)(c0 + j) * taps + k] : 0.0f;
+  // window[k] holds input row (t - (taps-1) + k) of [history; x]
+  auto load_row = [&](int pos, float (&v)[8]) {  // pos: position in [history; x]
+    if (pos < 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    } else if (pos < hrows) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = hist[(int64_t)pos * W + c0 + j];
+    } else {
+      const TI* src = x + (int64_t)(pos - hrows) * ldx + c0;
+      if (sizeof(TI) == 2) {
+        const half8 h = *reinterpret_cast<const half8*>(src);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(h[j]);
+      } else {
+        const float4_t a = *reinterpret_cast<const float4_t*>(src);
+        const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
+      }
+    }
+  };
+  float win[4][8];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) load_row(hrows + t0 - 3 + k, win[k + 1]);  // rows t0-3..t0-1
+  const int t1 = min(t0 + kConvRun, T);
+  for (int t = t0; t < t1; ++t) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[k][j] = win[k + 1][j];
+    load_row(hrows + t, win[3]);
+    TO out[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float acc = 0.0f;  // taps oldest -> newest, each product rounded before the add
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int tap = k - (4 - taps);  // window slot k holds delay 3-k
+        if (tap >= 0 && hrows + t - (3 - k) >= 0) acc = __fadd_rn(acc, __fmul_rn(win[k][j], wt[j][tap]));
+      }
+      out[j] = static_cast<TO>(acc / (1.0f + expf(-acc)));
+    }
+    TO* dst = y + (int64_t)t * ldy + c0;
+    if (sizeof(TO) == 2) {
+      half8 h;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(out[j]);
+      *reinterpret_cast<half8*>(dst) = h;
+    } else {
+      float4_t a, b;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = static_cast<float>(out[j]), b[j] = static_cast<float>(out[4 + j]);
+      *reinterpret_cast<float4_t*>(dst) = a;
+      *reinterpret_cast<float4_t*>(dst + 4) = b;
+    }
+  }
+}
+
+// Row RMSNorm with the row held in registers: one wave per row, VPL values
+// per lane loaded as 4-wide vectors (width == 4 * 64 * (VPL/4) exactly).
+template <int VPL, class TO>
+__global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restrict__ x, int64_t ldx,
+                                                           const float* __restrict__ w, TO* __restrict__ y,
+                                                           int64_t ldy, int rows, int width, float eps,
+                                                           float inv_width) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float v[VPL];
+  const float* src = x + (int64_t)row * ldx;
+#pragma unroll
+  for (int i = 0; i < VPL / 4; ++i) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(src + (i * 64 + lane) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i * 4 + j] = a[j];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) s += v[i] * v[i];
+  s = wave_sum(s);
+  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  TO* dst = y + (int64_t)row * ldy;
+#pragma unroll
+  for (int i = 0; i < VPL / 4; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    const float4_t ww = *reinterpret_cast<const float4_t*>(w + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[c + j] = static_cast<TO>(__fmul_rn(__fmul_rn(v[i * 4 + j], inverse), ww[j]));
+  }
+}
+
+// Gated output norm for rows of 128: 16 lanes per row, 8 values per lane.
+template <class TZ, class TO>
+__global__ __launch_bounds__(256) void gated_rms128_kernel(const float* __restrict__ o, const TZ* __restrict__ z,
+                                                           int64_t ldz, const float* __restrict__ w,
+                                                           TO* __restrict__ y, int T, int Hv, float eps) {
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (row >= T * Hv) return;
+  const int t = row / Hv, h = row % Hv;
+  const int c = sub * 8;
+  const float* src = o + (int64_t)row * 128 + c;
+  const float4_t a = *reinterpret_cast<const float4_t*>(src);
+  const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
+  const bool half_out = sizeof(TO) == 2;
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
+  if (half_out) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(static_cast<half_t>(v[j]));
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += v[j] * v[j];
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
+  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, 1.0f / 128.0f), eps));
+  float zf[8];
+  const TZ* zs = z + (int64_t)t * ldz + (int64_t)h * 128 + c;
+  if (sizeof(TZ) == 2) {
+    const half8 zh = *reinterpret_cast<const half8*>(zs);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) zf[j] = static_cast<float>(zh[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) zf[j] = static_cast<float>(zs[j]);
+  }
+  TO out[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float n = __fmul_rn(__fmul_rn(v[j], inverse), w[c + j]);
+    if (half_out) n = static_cast<float>(static_cast<half_t>(n));
+    out[j] = static_cast<TO>(__fmul_rn(n, zf[j] / (1.0f + expf(-zf[j]))));
+  }
+  TO* dst = y + (int64_t)row * 128 + c;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dst[j] = out[j];
+}
+
 // ---- decay and write strength (qwen.rs:619-627) -----------------------------
 __global__ __launch_bounds__(256) void gates_kernel(const void* a, int64_t lda, const void* b,
                                                     int64_t ldb, int dti, const float* dt,
@@ -203,6 +360,30 @@ extern "C" int clef_rms_norm(const void* x, int64_t ldx, int dtype_in, const flo
   CLEF_REQUIRE(rows >= 1 && width >= 1 && ldx >= width && ldy >= width, "RMS: dimensions");
   CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "RMS: dtype");
   CLEF_REQUIRE(eps > 0.0f && eps <= 1.0f, "RMS: epsilon");
+  const float inv_w = static_cast<float>(1.0 / static_cast<double>(width));
+  const bool vec = dtype_in == CLEF_F32 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+  if (vec && (width == 2048 || width == 1024)) {
+    const dim3 g((rows + 3) / 4);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const float* xf = static_cast<const float*>(x);
+    if (width == 2048) {
+      if (dtype_out == CLEF_F16)
+        hipLaunchKernelGGL((rms_f32_rows_kernel<32, half_t>), g, dim3(256), 0, st, xf, ldx, w,
+                           static_cast<half_t*>(y), ldy, rows, width, eps, inv_w);
+      else
+        hipLaunchKernelGGL((rms_f32_rows_kernel<32, float>), g, dim3(256), 0, st, xf, ldx, w,
+                           static_cast<float*>(y), ldy, rows, width, eps, inv_w);
+    } else {
+      if (dtype_out == CLEF_F16)
+        hipLaunchKernelGGL((rms_f32_rows_kernel<16, half_t>), g, dim3(256), 0, st, xf, ldx, w,
+                           static_cast<half_t*>(y), ldy, rows, width, eps, inv_w);
+      else
+        hipLaunchKernelGGL((rms_f32_rows_kernel<16, float>), g, dim3(256), 0, st, xf, ldx, w,
+                           static_cast<float*>(y), ldy, rows, width, eps, inv_w);
+    }
+    return check_launch("rms_norm");
+  }
   hipLaunchKernelGGL(rms_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, x, ldx,
                      dtype_in, w, y, ldy, dtype_out, rows, width, eps,
                      static_cast<float>(1.0 / static_cast<double>(width)));
@@ -220,6 +401,25 @@ extern "C" int clef_conv_silu(const void* x, int64_t ldx, int dtype_in, const fl
                    (history_rows == 0 || history),
                "conv: taps or history");
   CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "conv: dtype");
+  const bool vec = taps <= 4 && W % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  if (vec) {
+    const dim3 g((W / 8 + 255) / 256, (T + kConvRun - 1) / kConvRun);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (dtype_in == CLEF_F16 && dtype_out == CLEF_F16)
+      hipLaunchKernelGGL((conv_silu_vec_kernel<half_t, half_t>), g, dim3(256), 0, st, static_cast<const half_t*>(x),
+                         ldx, history, history_rows, w, taps, static_cast<half_t*>(y), ldy, T, W);
+    else if (dtype_in == CLEF_F16)
+      hipLaunchKernelGGL((conv_silu_vec_kernel<half_t, float>), g, dim3(256), 0, st, static_cast<const half_t*>(x),
+                         ldx, history, history_rows, w, taps, static_cast<float*>(y), ldy, T, W);
+    else if (dtype_out == CLEF_F16)
+      hipLaunchKernelGGL((conv_silu_vec_kernel<float, half_t>), g, dim3(256), 0, st, static_cast<const float*>(x),
+                         ldx, history, history_rows, w, taps, static_cast<half_t*>(y), ldy, T, W);
+    else
+      hipLaunchKernelGGL((conv_silu_vec_kernel<float, float>), g, dim3(256), 0, st, static_cast<const float*>(x),
+                         ldx, history, history_rows, w, taps, static_cast<float*>(y), ldy, T, W);
+    return check_launch("conv_silu");
+  }
   const int64_t n = (int64_t)T * W;
   hipLaunchKernelGGL(conv_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, x, ldx, dtype_in, history, history_rows, w, taps, y, ldy,
@@ -247,6 +447,24 @@ extern "C" int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, i
   CLEF_REQUIRE(o && z && w && y, "gated norm: null pointer");
   CLEF_REQUIRE(T >= 1 && Hv >= 1 && width >= 1 && ldz >= (int64_t)Hv * width, "gated norm: dimensions");
   CLEF_REQUIRE(dtype_ok(dtype_z) && dtype_ok(dtype_out), "gated norm: dtype");
+  if (width == 128 && ldz % 8 == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
+    const dim3 g((T * Hv + 15) / 16);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (dtype_z == CLEF_F16 && dtype_out == CLEF_F16)
+      hipLaunchKernelGGL((gated_rms128_kernel<half_t, half_t>), g, dim3(256), 0, st, o,
+                         static_cast<const half_t*>(z), ldz, w, static_cast<half_t*>(y), T, Hv, eps);
+    else if (dtype_z == CLEF_F16)
+      hipLaunchKernelGGL((gated_rms128_kernel<half_t, float>), g, dim3(256), 0, st, o,
+                         static_cast<const half_t*>(z), ldz, w, static_cast<float*>(y), T, Hv, eps);
+    else if (dtype_out == CLEF_F16)
+      hipLaunchKernelGGL((gated_rms128_kernel<float, half_t>), g, dim3(256), 0, st, o,
+                         static_cast<const float*>(z), ldz, w, static_cast<half_t*>(y), T, Hv, eps);
+    else
+      hipLaunchKernelGGL((gated_rms128_kernel<float, float>), g, dim3(256), 0, st, o,
+                         static_cast<const float*>(z), ldz, w, static_cast<float*>(y), T, Hv, eps);
+    return check_launch("gated_rms_silu");
+  }
   hipLaunchKernelGGL(gated_rms_kernel, dim3((T * Hv + 3) / 4), dim3(256), 0, (hipStream_t)stream, o,
                      z, ldz, dtype_z, w, y, dtype_out, T, Hv, width, eps,
                      static_cast<float>(1.0 / static_cast<double>(width)));

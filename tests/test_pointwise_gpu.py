@@ -1,0 +1,139 @@
+"""Parity of the kernels around the scan and the attention core against the
+oracle (f32) and the reference's rounding points (f16 activations)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+gpu = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def clef():
+    import clef_hip
+    clef_hip.lib()
+    return clef_hip
+
+
+def _silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+@gpu
+@pytest.mark.parametrize("W,T,hist", [(8192, 139, 0), (8192, 17, 3), (8192, 2, 1), (64, 33, 2),
+                                      (16, 5, 0), (3, 4, 0)])
+@pytest.mark.parametrize("dt_in,dt_out", [(torch.float32, torch.float32), (torch.float16, torch.float16),
+                                          (torch.float16, torch.float32)])
+def test_conv_silu_matches_oracle(clef, W, T, hist, dt_in, dt_out):
+    """pointwise.rs:330-358 shapes; history rows precede the tokens (resume)."""
+    gen = torch.Generator(device="cuda").manual_seed(W + T)
+    x = torch.sin(torch.arange(T * W, device="cuda", dtype=torch.float32) * 0.073).reshape(T, W).to(dt_in)
+    w = torch.cos(torch.arange(W * 4, device="cuda", dtype=torch.float32) * 0.027).reshape(W, 1, 4)
+    h = torch.randn((hist, W), generator=gen, device="cuda") if hist else None
+    y = clef.conv_silu(x, w, history=h, out_dtype=dt_out)
+    full = np.concatenate([h.cpu().numpy(), x.float().cpu().numpy()]) if hist else x.float().cpu().numpy()
+    exp = oracle.causal_conv(full, w.cpu().numpy())[hist:]
+    exp = _silu(exp.astype(np.float64))
+    got = y.float().cpu().numpy()
+    if dt_out == torch.float32:
+        np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6)
+    else:
+        np.testing.assert_allclose(got, exp, rtol=2e-3, atol=1e-3)
+
+
+@gpu
+@pytest.mark.parametrize("rows,width", [(4096, 2048), (17, 1024), (139, 16), (3, 4096)])
+@pytest.mark.parametrize("dt_out", [torch.float32, torch.float16])
+def test_rms_matches_oracle(clef, rows, width, dt_out):
+    """pointwise.rs:430-466 generator: x = sin(0.073 i), w = 0.7."""
+    x = torch.sin(torch.arange(rows * width, device="cuda", dtype=torch.float32) * 0.073).reshape(rows, width)
+    w = torch.full((width,), 0.7, device="cuda")
+    y = clef.rms_norm(x, w, out_dtype=dt_out)
+    exp = oracle.rms(x.cpu().numpy(), w.cpu().numpy())
+    if dt_out == torch.float32:
+        # the oracle sums sequentially, the kernel in a tree: compare both with the
+        # exact (f64) result at the reference's 1e-6 bar (pointwise.rs:455) and
+        # with each other within the f32 summation error of a 4096-wide row
+        xd = x.double().cpu().numpy()
+        exact = xd / np.sqrt((xd ** 2).mean(-1, keepdims=True) + 1e-6) * 0.7
+        assert np.abs(y.cpu().numpy() - exact).max() <= 1e-6
+        assert np.abs(y.cpu().numpy() - exp).max() <= 4e-6
+    else:  # one half ulp at most after rounding
+        np.testing.assert_allclose(y.float().cpu().numpy(), exp, rtol=2 ** -10, atol=2 ** -24)
+
+
+@gpu
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("T,Hv,width", [(300, 32, 128), (20, 2, 4), (7, 3, 64)])
+def test_gated_rms_silu(clef, dt, T, Hv, width):
+    gen = torch.Generator(device="cuda").manual_seed(T)
+    o = torch.randn((T, Hv, width), generator=gen, device="cuda")
+    z = torch.randn((T, Hv * width), generator=gen, device="cuda").to(dt)
+    w = torch.randn((width,), generator=gen, device="cuda")
+    y = clef.gated_rms_silu(o, z, w, out_dtype=dt)
+    on = o.to(dt).float().cpu().numpy()
+    n = oracle.rms(on.reshape(-1, width), w.cpu().numpy()).reshape(T, Hv * width)
+    zf = z.float().cpu().numpy()
+    if dt == torch.float16:
+        n = n.astype(np.float16).astype(np.float32)
+    exp = n * _silu(zf.astype(np.float64))
+    tol = 1e-5 if dt == torch.float32 else 2e-3
+    np.testing.assert_allclose(y.float().cpu().numpy(), exp, rtol=tol, atol=tol)
+
+
+@gpu
+@pytest.mark.parametrize("heads,kvh,qn,kn,d", [(16, 2, 300, 300, 256), (2, 1, 20, 20, 8), (4, 2, 17, 273, 64),
+                                               (2, 1, 1, 256, 256), (8, 8, 130, 130, 128)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_attention_gated_matches_oracle(clef, heads, kvh, qn, kn, d, dt):
+    """ops.rs:62-148 tiled attention (lower-right causal mask with cached keys), gated."""
+    gen = torch.Generator(device="cuda").manual_seed(qn * 7 + kn)
+    q = torch.randn((heads, qn, d), generator=gen, device="cuda").to(dt)
+    k = torch.randn((kvh, kn, d), generator=gen, device="cuda").to(dt)
+    v = torch.randn((kvh, kn, d), generator=gen, device="cuda").to(dt)
+    proj = torch.randn((qn, heads, 2 * d), generator=gen, device="cuda").to(dt)
+    gate = proj[:, :, d:]
+    vt = clef.values_transposed(v.permute(1, 0, 2).contiguous().reshape(kn, kvh * d), kvh, d)
+    y = clef.attention_gated(q, k, vt, gate)
+    att = oracle.attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), True)
+    att = att.transpose(1, 0, 2).reshape(qn, heads * d)
+    g = gate.float().cpu().numpy().reshape(qn, heads * d)
+    sig = 1.0 / (1.0 + np.exp(-g.astype(np.float64)))
+    if dt == torch.float16:
+        exp = att.astype(np.float16).astype(np.float64) * sig.astype(np.float16).astype(np.float64)
+        np.testing.assert_allclose(y.float().cpu().numpy(), exp, rtol=1e-2, atol=5e-3)
+    else:
+        np.testing.assert_allclose(y.cpu().numpy(), att * sig, rtol=1e-4, atol=1e-5)
+
+
+@gpu
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_qk_norm_rotary_matches_oracle(clef, dt):
+    T, heads, d, rot, pos0 = 37, 4, 256, 64, 11
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    proj = torch.randn((T, heads, 2 * d), generator=gen, device="cuda").to(dt)
+    w = 1.0 + 0.1 * torch.randn((d,), generator=gen, device="cuda")
+    y = clef.qk_norm_rotary(proj, heads, d, w, rot, 1e7, pos0=pos0, head_stride=2 * d)
+    q = proj[:, :, :d].float().cpu().numpy()
+    n = oracle.rms(q.reshape(-1, d), w.cpu().numpy()).reshape(T, heads, d)
+    if dt == torch.float16:
+        n = n.astype(np.float16).astype(np.float32)
+    exp = oracle.rotary(n, rot, 1e7, pos0=pos0).transpose(1, 0, 2)
+    tol = 1e-5 if dt == torch.float32 else 2e-3
+    np.testing.assert_allclose(y.float().cpu().numpy(), exp, rtol=tol, atol=tol)
+
+
+@gpu
+def test_delta_gates_matches_reference_formula(clef):
+    T, Hv = 333, 32
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    ab = (torch.randn((T, 2 * Hv + 5), generator=gen, device="cuda") * 4).half()
+    dt = torch.randn(Hv, generator=gen, device="cuda")
+    alog = torch.randn(Hv, generator=gen, device="cuda")
+    g, beta = clef.delta_gates(ab[:, :Hv], ab[:, Hv:2 * Hv], dt, alog)
+    a = ab[:, :Hv].double().cpu() + dt.double().cpu()
+    sp = a.clamp(min=0) + torch.log1p(torch.exp(-a.abs()))
+    np.testing.assert_allclose(g.cpu().numpy(), (sp * -torch.exp(alog.double().cpu())).numpy(), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(beta.cpu().numpy(), torch.sigmoid(ab[:, Hv:2 * Hv].double().cpu()).numpy(),
+                               rtol=1e-6, atol=1e-7)
