@@ -51,7 +51,7 @@ static int scan_dims(int T, int Hk, int Hv, int dk, int dv, int chunk, int preci
 extern "C" size_t clef_delta_scan_workspace(int T, int Hk, int Hv, int dk, int dv, int chunk,
                                             int precision) {
   if (scan_dims(T, Hk, Hv, dk, dv, chunk, precision)) return 0;
-  return clef::scan_workspace_bytes(T, Hk, Hv, precision);
+  return clef::scan_workspace_bytes(T, Hk, Hv, dk, precision);
 }
 
 extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk,
@@ -74,7 +74,7 @@ extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int6
                "DeltaNet scan: token stride smaller than a token row");
   CLEF_REQUIRE(capture >= 0 && capture <= T, "DeltaNet scan: capture must be in 0..T");
   CLEF_REQUIRE(capture == 0 || captured, "DeltaNet scan: capture requested without a buffer");
-  const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, precision);
+  const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, dk, precision);
   CLEF_REQUIRE(workspace && workspace_bytes >= need, "DeltaNet scan: workspace too small");
   CLEF_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
                "DeltaNet scan: workspace must be 256-byte aligned");

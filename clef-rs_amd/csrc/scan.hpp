@@ -24,14 +24,18 @@ struct ScanParams {
   float* captured;
   float* final_state;
   // workspace views
-  void* Tm;     // [nchunks][Hv][64][64] compute dtype: (I + A)^-1
-  void* Mm;     // [nchunks][Hv][64][64] compute dtype: masked decayed Q K^T
-  float* gam;   // [nchunks][Hv][64]   in-chunk cumulative log-decay
-  float* invk;  // [nchunks][Hk][64]   1/|k|
-  float* scq;   // [nchunks][Hk][64]   qscale/|q|
+  void* Tm;      // [nchunks][Hv][64][64] compute dtype: (I + A)^-1
+  void* Mm;      // [nchunks][Hv][64][64] compute dtype: masked decayed Q K^T
+  void* Kt;      // [nchunks][Hk][DK][64] compute dtype: normalised K^T
+  float* eg;     // [nchunks][Hv][64]   exp(gam_r)
+  float* wl;     // [nchunks][Hv][64]   exp(gam_last - gam_r)
+  float* bt;     // [nchunks][Hv][64]   beta
+  float* gam_ws; // [nchunks][Hv][64]   in-chunk cumulative log-decay
+  float* invk;   // [nchunks][Hk][64]   1/|k| (0 on padding rows)
+  float* scq;    // [nchunks][Hk][64]   qscale/|q| (0 on padding rows)
 };
 
-size_t scan_workspace_bytes(int T, int Hk, int Hv, int precision);
+size_t scan_workspace_bytes(int T, int Hk, int Hv, int dk, int precision);
 void scan_carve_workspace(ScanParams& p, void* ws, int precision);
 int scan_launch(const ScanParams& p, int precision, hipStream_t stream);
 
