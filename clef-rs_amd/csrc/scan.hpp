@@ -23,16 +23,14 @@ struct ScanParams {
   void* out;
   float* captured;
   float* final_state;
-  // workspace views
-  void* Tm;      // [nchunks][Hv][64][64] compute dtype: (I + A)^-1
-  void* Mm;      // [nchunks][Hv][64][64] compute dtype: masked decayed Q K^T
-  void* Kt;      // [nchunks][Hk][DK][64] compute dtype: normalised K^T
-  float* eg;     // [nchunks][Hv][64]   exp(gam_r)
-  float* wl;     // [nchunks][Hv][64]   exp(gam_last - gam_r)
-  float* bt;     // [nchunks][Hv][64]   beta
-  float* gam_ws; // [nchunks][Hv][64]   in-chunk cumulative log-decay
-  float* invk;   // [nchunks][Hk][64]   1/|k| (0 on padding rows)
-  float* scq;    // [nchunks][Hk][64]   qscale/|q| (0 on padding rows)
+  // Workspace views.  A "block" is one MFMA operand fragment of a 64-lane
+  // wave: 64 x 16 bytes, lane-major, in the compute dtype.
+  void* Kf;   // [chunks][Hk][4 x dk-blocks]  normalised keys  (rows of X = K^ S)
+  void* Qf;   // [chunks][Hk][4 x dk-blocks]  scaled normalised queries
+  void* Uf;   // [chunks][Hv][state tiles x token blocks]  U = K^T W (I+A)^-1
+  void* Nf;   // [chunks][Hv][4 x token blocks]            N = M (I+A)^-1
+  void* Ucf;  // [Hv][state tiles x token blocks]  U weighted for the capture token
+  float* sc;  // [chunks][Hv][4][64]  beta, exp(gam), gam, 0
 };
 
 size_t scan_workspace_bytes(int T, int Hk, int Hv, int dk, int precision);
