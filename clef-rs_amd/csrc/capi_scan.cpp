@@ -73,8 +73,8 @@ extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int6
                    sgb >= Hv && so >= static_cast<int64_t>(Hv) * dv,
                "DeltaNet scan: token stride smaller than a token row");
   // a chunk's rows of v and out are addressed with 32-bit byte offsets
-  CLEF_REQUIRE(sv < (int64_t(1) << 23) && so < (int64_t(1) << 23),
-               "DeltaNet scan: token stride of v or out above 2^23 elements");
+  CLEF_REQUIRE(sv < (int64_t(1) << 22) && so < (int64_t(1) << 22),
+               "DeltaNet scan: token stride of v or out above 2^22 elements");
   CLEF_REQUIRE(capture >= 0 && capture <= T, "DeltaNet scan: capture must be in 0..T");
   CLEF_REQUIRE(capture == 0 || captured, "DeltaNet scan: capture requested without a buffer");
   const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, dk, precision);
