@@ -10,9 +10,9 @@
 //   A[r][c] = beta_r (k^_r.k^_c) exp(gam_r - gam_c)  (c < r);  Tm = (I + A)^-1
 //   M[r][c] = (q^_r.k^_c) exp(gam_r - gam_c)          (c <= r)
 //   W       = diag(exp(gam_last - gam))
-//   U       = K^^T W Tm            (dk x C)
-//   N       = M Tm                 (C x C)
-//   Y       = diag(beta) (V - diag(exp gam) K^ S)
+//   U       = K^^T W Tm diag(beta) (dk x C)
+//   N       = M Tm diag(beta)      (C x C)
+//   Y       = V - diag(exp gam) K^ S
 //   O       = diag(exp gam) Q^ S + N Y
 //   S'      = exp(gam_last) S + U Y
 // Decay ratios are only formed for c <= r, so g = -1000 underflows to exact
@@ -89,15 +89,16 @@ __device__ __forceinline__ half8 pack_frag(const float4_t* acc, int kb, half_t) 
   return f;
 }
 
-// EPF consecutive f32 values (times optional weights) as a CT fragment.
-__device__ __forceinline__ float4_t frag_from_f32(const float* x, const float* w, float) {
-  float4_t a = *reinterpret_cast<const float4_t*>(x);
+// EPF consecutive f32 values times a scale (and optional per-element
+// weights) as a CT fragment.
+__device__ __forceinline__ float4_t frag_from_f32(const float* x, const float* w, float scale, float) {
+  float4_t a = *reinterpret_cast<const float4_t*>(x) * scale;
   if (w) a = a * *reinterpret_cast<const float4_t*>(w);
   return a;
 }
-__device__ __forceinline__ half8 frag_from_f32(const float* x, const float* w, half_t) {
-  float4_t a = *reinterpret_cast<const float4_t*>(x);
-  float4_t b = *reinterpret_cast<const float4_t*>(x + 4);
+__device__ __forceinline__ half8 frag_from_f32(const float* x, const float* w, float scale, half_t) {
+  float4_t a = *reinterpret_cast<const float4_t*>(x) * scale;
+  float4_t b = *reinterpret_cast<const float4_t*>(x + 4) * scale;
   if (w) {
     a = a * *reinterpret_cast<const float4_t*>(w);
     b = b * *reinterpret_cast<const float4_t*>(w + 4);
@@ -136,6 +137,11 @@ __device__ __forceinline__ float bits_to_f32(uint32_t b, int dtype) {
   const uint16_t h = static_cast<uint16_t>(b);
   return static_cast<float>(*reinterpret_cast<const half_t*>(&h));
 }
+
+// e^x for decay factors: hardware 2^x (1 ulp) of x log2(e).  Callers pass
+// differences of cumulative log-decays, formed before scaling so they keep
+// full precision; results below the normal range may flush to zero.
+__device__ __forceinline__ float decay_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -304,12 +310,14 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     gram[s] = acc;
   }
   lds_barrier();  // sK / sQ are dead from here on
-  // zeros that no v-head rewrites: lower blocks of sTT (Tm above the
-  // diagonal blocks) and upper tiles of sM
-  for (int idx = tid; idx < kC * kC; idx += 256) {
-    const int a = idx >> 6, b = idx & 63;
-    if ((b >> 4) < (a >> 4)) sTT[a * LDF + b] = 0.0f;
-    if ((b >> 4) > (a >> 4)) sM[a * LDT + b] = CT(0);
+  // zeros that no v-head rewrites: the six 16x16 blocks of sTT below its
+  // diagonal blocks (Tm above them) and the six tiles of sM above its diagonal
+  for (int e = tid; e < 6 * 256; e += 256) {
+    const int blk = e >> 8, ra = (e >> 4) & 15, cb = e & 15;
+    const int hi = blk >= 3 ? 3 : blk >= 1 ? 2 : 1;  // (hi, lo): (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
+    const int lo = blk - hi * (hi - 1) / 2;
+    sTT[(16 * hi + ra) * LDF + 16 * lo + cb] = 0.0f;
+    sM[(16 * lo + ra) * LDT + 16 * hi + cb] = CT(0);
   }
 
   // ---- 3. per v-head
@@ -335,11 +343,11 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       const float gcap = __shfl(cs, cap_row, 64);
       sGam[lane] = cs;
       sBeta[lane] = bv;
-      sW[lane] = expf(gl - cs);
-      if (chunk == cap_chunk) sWc[lane] = lane <= cap_row ? expf(gcap - cs) : 0.0f;
+      sW[lane] = decay_exp(gl - cs);
+      if (chunk == cap_chunk) sWc[lane] = lane <= cap_row ? decay_exp(gcap - cs) : 0.0f;
       float* sc = p.sc + cv * 256;
       sc[lane] = bv;
-      sc[64 + lane] = expf(cs);
+      sc[64 + lane] = decay_exp(cs);
       sc[128 + lane] = cs;
       sc[192 + lane] = 0.0f;
     }
@@ -357,7 +365,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * tr + 4 * grp + i;
-        const float d = (c <= r) ? expf(sGam[r] - gc) : 0.0f;
+        const float d = (c <= r) ? decay_exp(sGam[r] - gc) : 0.0f;
         if (!isqk)
           sA[r * LDF + c] = (c < r) ? (sBeta[r] * gram[s][i]) * d : 0.0f;
         else
@@ -405,7 +413,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       }
       lds_barrier();
     }
-    // 3d. U blocks (s, b): U[slot(s, m)][token block b], as U^T = (W Tm)^T K^
+    // 3d. U blocks (s, b): U[slot(s, m)][token block b], as U^T = (W Tm B)^T K^
     //     on MFMA; token tiles of block b are TPK*b + u.  Tm[r][c] = 0 for
     //     r < c, so token blocks kr < b contribute nothing.
     auto u_blocks = [&](const float* wts, frag* dst) {
@@ -420,7 +428,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
         for (int kr = 0; kr < NKT; ++kr)
           if (kr >= b) {
             const int c = slot_index<CT>(TPK * b + u, col);
-            af[u][kr] = frag_from_f32(sTT + c * LDF + kr * KB + grp * EPF, wts + kr * KB + grp * EPF, CT(0));
+            af[u][kr] = frag_from_f32(sTT + c * LDF + kr * KB + grp * EPF, wts + kr * KB + grp * EPF, sBeta[c], CT(0));
           }
 #pragma unroll
       for (int ss = 0; ss < SPW; ++ss) {
@@ -441,7 +449,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     };
     u_blocks(sW, static_cast<frag*>(p.Uf) + cv * G::NBU * 64);
     if (chunk == cap_chunk) u_blocks(sWc, static_cast<frag*>(p.Ucf) + (int64_t)h * G::NBU * 64);
-    // 3e. N blocks (t, b): N[16t + m][token block b], as N^T = Tm^T M^T;
+    // 3e. N blocks (t, b): N[16t + m][token block b], as N^T = (Tm B)^T M^T;
     //     wave t.  Nonzero terms need c' <= k <= r.
     {
       const int t = wave;
@@ -460,7 +468,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
 #pragma unroll
           for (int kb = 0; kb < NKT; ++kb)
             if (kb >= b && kb <= kmax)
-              Mma<CT>::mma(acc[u], frag_from_f32(sTT + c * LDF + kb * KB + grp * EPF, nullptr, CT(0)), bm[kb]);
+              Mma<CT>::mma(acc[u], frag_from_f32(sTT + c * LDF + kb * KB + grp * EPF, nullptr, sBeta[c], CT(0)), bm[kb]);
         }
         dst[(t * NKT + b) * 64 + lane] = pack_frag(acc, 0, CT(0));
       }
@@ -479,6 +487,7 @@ struct Carry {
   static constexpr int D0 = sizeof(CT) == 2 ? 3 : 2;   // ring slots
   static constexpr int NL = G::NBK + G::NBU + 1;       // blocks per slot (+ scalars)
   static constexpr int NH = G::NKX + G::NKT;           // hand-off blocks: S, Y
+  static constexpr int SLOT = NL * 64;                 // ring slot, 16-byte units
   static_assert((D0 - 2) * NL < 64, "ring wait count must fit vmcnt");
 };
 
@@ -496,7 +505,7 @@ __device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx
   typedef Carry<CT, DK> K;
   typedef typename K::G G;
   auto issue = [&](int c) {
-    typename K::frag* slot = ring + (c % K::D0) * K::NL * 64;
+    typename K::frag* slot = ring + (c % K::D0) * K::SLOT;
     const char* kf = static_cast<const char*>(p.Kf) + (((int64_t)c * p.Hk + x.hk) * G::NBK * 64 + x.lane) * 16;
     const char* uf = static_cast<const char*>(p.Uf) + (((int64_t)c * p.Hv + x.h) * G::NBU * 64 + x.lane) * 16;
     const char* sc = reinterpret_cast<const char*>(p.sc + ((int64_t)c * p.Hv + x.h) * 256) + x.lane * 16;
@@ -530,7 +539,7 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
   typedef Carry<CT, DK> K;
   typedef typename K::G G;
   typedef typename K::frag frag;
-  constexpr int NST = G::NST, NKX = G::NKX, NKT = G::NKT, NBK = G::NBK, NBU = G::NBU;
+  constexpr int NST = G::NST, NKX = G::NKX, NKT = G::NKT, NBK = G::NBK, NBU = G::NBU, TPK = G::TPK;
   const int lane = x.lane, grp = x.grp;
   const int dk = p.dk, dv = p.dv;
 
@@ -570,55 +579,71 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
   lds_barrier();  // prologue
 
   auto step = [&](int i, uint32_t* vbuf) {
-    const frag* slot = ring + (i % K::D0) * K::NL * 64;
+    const frag* slot = ring + (i % K::D0) * K::SLOT;
     const float* scs = reinterpret_cast<const float*>(slot + (NBK + NBU) * 64);  // beta, eg, gam
     // every LDS operand of the chunk is requested before the first product,
     // so the reads overlap each other and the MFMAs instead of serialising
     frag kfr[4][NKX], ufr[NST][NKT];
-    float4_t bt[4], eg[4];
+    float4_t eg[4];
 #pragma unroll
     for (int kb = 0; kb < NKX; ++kb)
 #pragma unroll
       for (int t = 0; t < 4; ++t) kfr[t][kb] = slot[(t * NKX + kb) * 64 + lane];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int base = slot_index<CT>(t, 4 * grp);
-      bt[t] = *reinterpret_cast<const float4_t*>(scs + base);
-      eg[t] = *reinterpret_cast<const float4_t*>(scs + 64 + base);
-    }
+    for (int t = 0; t < 4; ++t) eg[t] = *reinterpret_cast<const float4_t*>(scs + 64 + slot_index<CT>(t, 4 * grp));
     const float el = scs[64 + kC - 1];
+    // hand S_i to the output waves
+    frag* hs = hand + (i & 1) * K::NH * 64;
+#pragma unroll
+    for (int kb = 0; kb < NKX; ++kb) hs[kb * 64 + lane] = Sf[kb];
     __builtin_amdgcn_sched_barrier(0);
     // X = K^ S (token rows in slot order)
     float4_t X[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    // (rounds of 4 independent accumulators, fenced so the scheduler cannot
+    // turn them into dependent chains)
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb)
+    for (int kb = 0; kb < NKX; ++kb) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kfr[t][kb], Sf[kb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // U is requested while the products run (its registers replace K^'s)
 #pragma unroll
     for (int s = 0; s < NST; ++s)
 #pragma unroll
       for (int b = 0; b < NKT; ++b) ufr[s][b] = slot[(NBK + s * NKT + b) * 64 + lane];
     __builtin_amdgcn_sched_barrier(0);
-    // Y = beta (V - exp(gam) X); padding rows have beta = 0
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) X[t][j] = bt[t][j] * (bits_value<IT>(vbuf[4 * t + j]) - eg[t][j] * X[t][j]);
+    // Y = V - exp(gam) X (beta is folded into U and N) for token block b
     frag Yf[NKT];
+    auto y_block = [&](int b) {
 #pragma unroll
-    for (int b = 0; b < NKT; ++b) Yf[b] = pack_frag(X, b, CT(0));
-    // hand S_i and Y_i to the output waves
-    frag* hs = hand + (i & 1) * K::NH * 64;
+      for (int u = 0; u < TPK; ++u) {
+        const int t = TPK * b + u;
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) hs[kb * 64 + lane] = Sf[kb];
+        for (int j = 0; j < 4; ++j) X[t][j] = bits_value<IT>(vbuf[4 * t + j]) - eg[t][j] * X[t][j];
+      }
+      Yf[b] = pack_frag(X, b, CT(0));
+    };
+    if (i != x.cap_chunk) {
+      // S <- exp(gam_last) S + U Y: the scaling runs under the X products, and
+      // each token block's update starts as soon as its Y is packed
 #pragma unroll
-    for (int b = 0; b < NKT; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
-    // state after token `capture`: exp(gam_r*) S_i + Ucap Y_i
-    if (i == x.cap_chunk) {
-      const float ec = expf(scs[128 + x.cap_row]);
+      for (int s = 0; s < NST; ++s) S[s] = S[s] * el;
+#pragma unroll
+      for (int b = 0; b < NKT; ++b) {
+        y_block(b);
+#pragma unroll
+        for (int s = 0; s < NST; ++s) Mma<CT>::mma(S[s], ufr[s][b], Yf[b]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // capture chunk: the state after token `capture` is
+      // exp(gam_r*) S_i + Ucap Y_i, formed before S_i is updated
+#pragma unroll
+      for (int b = 0; b < NKT; ++b) y_block(b);
+      const float ec = decay_exp(scs[128 + x.cap_row]);
       const frag* uc = static_cast<const frag*>(p.Ucf) + (int64_t)x.h * NBU * 64 + lane;
 #pragma unroll
       for (int s = 0; s < NST; ++s) {
@@ -631,16 +656,172 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
           if (row < dk && x.col_ok) p.captured[((int64_t)x.h * dk + row) * dv + x.jc] = acc[j];
         }
       }
-    }
-    // S <- exp(gam_last) S + U Y
 #pragma unroll
-    for (int s = 0; s < NST; ++s) {
-      S[s] = S[s] * el;
+      for (int s = 0; s < NST; ++s) {
+        S[s] = S[s] * el;
 #pragma unroll
-      for (int b = 0; b < NKT; ++b) Mma<CT>::mma(S[s], ufr[s][b], Yf[b]);
+        for (int b = 0; b < NKT; ++b) Mma<CT>::mma(S[s], ufr[s][b], Yf[b]);
+      }
     }
 #pragma unroll
     for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
+    // hand Y_i to the output waves
+#pragma unroll
+    for (int b = 0; b < NKT; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
+    load_v(vbuf, i + 2);
+    lds_barrier();  // end of chunk i
+  };
+  int i = 0;
+  for (; i + 1 < x.nchunks; i += 2) {
+    step(i, va);
+    step(i + 1, vb);
+  }
+  if (i < x.nchunks) step(i, va);
+  lds_barrier();  // outputs of the last chunk
+
+  if (p.final_state) {
+#pragma unroll
+    for (int s = 0; s < NST; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = slot_index<CT>(s, 4 * grp + j);
+        if (row < dk && x.col_ok) p.final_state[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
+      }
+  }
+}
+
+// wave 0, f16 operands: the recurrence with the LDS reads of each round
+// interleaved with the MFMAs of the previous one (a wave issues one 1 KiB
+// read per ~14 cycles, an MFMA per 18).  IT = dtype of v.
+template <class CT, int DK, class IT>
+__device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const CarryCtx& x,
+                                                     const typename Carry<CT, DK>::frag* ring,
+                                                     typename Carry<CT, DK>::frag* hand) {
+  typedef Carry<CT, DK> K;
+  typedef typename K::G G;
+  typedef typename K::frag frag;
+  constexpr int NST = G::NST, NKX = G::NKX, NBK = G::NBK, NBU = G::NBU;
+  static_assert(G::NKT == 2 && G::TPK == 2, "f16 geometry");
+  const int lane = x.lane, grp = x.grp;
+  const int dk = p.dk, dv = p.dv;
+
+  float4_t S[NST];
+#pragma unroll
+  for (int s = 0; s < NST; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = slot_index<CT>(s, 4 * grp + i);
+      float v = 0.0f;
+      if (p.initial && row < dk && x.col_ok) v = p.initial[((int64_t)x.h * dk + row) * dv + x.jc];
+      S[s][i] = v;
+    }
+  frag Sf[NKX];
+#pragma unroll
+  for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
+
+  // v two chunks ahead in registers: byte offsets of this lane's 16 X-rows;
+  // rows past the end of the sequence fall outside the buffer range (read 0)
+  const IT* vbase = static_cast<const IT*>(p.v) + (int64_t)x.h * dv + x.j0;
+  int voff[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      voff[4 * q + j] = x.col_ok ? (slot_index<CT>(q, 4 * grp + j) * (int)p.sv + x.col) * (int)sizeof(IT) : kOOB;
+  auto load_v = [&](uint32_t* vb, int c) {
+    const int cc = min(c, x.nchunks - 1);
+    const int t0 = cc * kC, n = min(kC, p.T - t0);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(vbase + (int64_t)t0 * p.sv, n * (int)p.sv * (int)sizeof(IT));
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vb[k] = buffer_load_bits<IT>(r, voff[k]);
+  };
+  uint32_t va[16], vb[16];
+  load_v(va, 0);
+  load_v(vb, 1);
+  lds_barrier();  // prologue
+
+  auto step = [&](int i, uint32_t* vbuf) {
+    const frag* slot = ring + (i % K::D0) * K::SLOT;
+    const float* scs = reinterpret_cast<const float*>(slot + (NBK + NBU) * 64);  // beta, eg, gam
+    frag* hs = hand + (i & 1) * K::NH * 64;
+    frag kf[4][NKX], uf[NST][2];
+    float4_t eg[4], X[4];
+    float el;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) kf[t][0] = slot[(t * NKX) * 64 + lane];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_sched_barrier(0);
+    // X = K^ S in rounds of 4 independent products; each round also requests
+    // the next round's operands
+#pragma unroll
+    for (int kb = 0; kb < NKX; ++kb) {
+      if (kb + 1 < NKX) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kf[t][kb + 1] = slot[(t * NKX + kb + 1) * 64 + lane];
+      }
+      if (kb == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) eg[t] = *reinterpret_cast<const float4_t*>(scs + 64 + slot_index<CT>(t, 4 * grp));
+        el = scs[64 + kC - 1];
+      }
+      if (kb == NKX - 1) {
+#pragma unroll
+        for (int s = 0; s < NST; ++s) uf[s][0] = slot[(NBK + 2 * s) * 64 + lane];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kf[t][kb], Sf[kb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Y = V - exp(gam) X for token block b (beta is folded into U and N)
+    frag Yf[2];
+    auto y_block = [&](int b) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          X[2 * b + u][j] = bits_value<IT>(vbuf[4 * (2 * b + u) + j]) - eg[2 * b + u][j] * X[2 * b + u][j];
+      Yf[b] = pack_frag(X, b, CT(0));
+    };
+    y_block(0);
+    if (i == x.cap_chunk) {
+      // state after token `capture`: exp(gam_r*) S_i + Ucap Y_i
+      y_block(1);
+      const float ec = decay_exp(scs[128 + x.cap_row]);
+      const frag* uc = static_cast<const frag*>(p.Ucf) + (int64_t)x.h * NBU * 64 + lane;
+#pragma unroll
+      for (int s = 0; s < NST; ++s) {
+        float4_t acc = S[s] * ec;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) Mma<CT>::mma(acc, uc[(2 * s + b) * 64], Yf[b]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = slot_index<CT>(s, 4 * grp + j);
+          if (row < dk && x.col_ok) p.captured[((int64_t)x.h * dk + row) * dv + x.jc] = acc[j];
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // S <- exp(gam_last) S + U Y, token block 0 (requests U of block 1)
+#pragma unroll
+    for (int s = 0; s < NST; ++s) uf[s][1] = slot[(NBK + 2 * s + 1) * 64 + lane];
+#pragma unroll
+    for (int s = 0; s < NST; ++s) {
+      S[s] = S[s] * el;
+      Mma<CT>::mma(S[s], uf[s][0], Yf[0]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (i != x.cap_chunk) y_block(1);
+    // token block 1; S_i goes to the output waves meanwhile
+#pragma unroll
+    for (int kb = 0; kb < NKX; ++kb) hs[kb * 64 + lane] = Sf[kb];
+#pragma unroll
+    for (int s = 0; s < NST; ++s) Mma<CT>::mma(S[s], uf[s][1], Yf[1]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
+#pragma unroll
+    for (int b = 0; b < 2; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
     load_v(vbuf, i + 2);
     lds_barrier();  // end of chunk i
   };
@@ -739,7 +920,7 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
 template <class CT, int DK>
 __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   typedef Carry<CT, DK> K;
-  __shared__ __attribute__((aligned(16))) typename K::frag ring[K::D0 * K::NL * 64];
+  __shared__ __attribute__((aligned(16))) typename K::frag ring[K::D0 * K::SLOT];
   __shared__ __attribute__((aligned(16))) typename K::frag hand[2 * K::NH * 64];
 
   CarryCtx x;
@@ -766,10 +947,17 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   if (wave == 1) {
     carry_loader<CT, DK>(p, x, ring);
   } else if (wave == 0) {
-    if (p.dtype_qkv == 0)
-      carry_recurrence<CT, DK, float>(p, x, ring, hand);
-    else
-      carry_recurrence<CT, DK, half_t>(p, x, ring, hand);
+    if constexpr (sizeof(CT) == 2) {
+      if (p.dtype_qkv == 0)
+        carry_recurrence_f16<CT, DK, float>(p, x, ring, hand);
+      else
+        carry_recurrence_f16<CT, DK, half_t>(p, x, ring, hand);
+    } else {
+      if (p.dtype_qkv == 0)
+        carry_recurrence<CT, DK, float>(p, x, ring, hand);
+      else
+        carry_recurrence<CT, DK, half_t>(p, x, ring, hand);
+    }
   } else {
     if (p.dtype_out == 0)
       carry_outputs<CT, DK, float>(p, x, wave - 2, hand);

@@ -27,8 +27,8 @@ struct ScanParams {
   // wave: 64 x 16 bytes, lane-major, in the compute dtype.
   void* Kf;   // [chunks][Hk][4 x dk-blocks]  normalised keys  (rows of X = K^ S)
   void* Qf;   // [chunks][Hk][4 x dk-blocks]  scaled normalised queries
-  void* Uf;   // [chunks][Hv][state tiles x token blocks]  U = K^T W (I+A)^-1
-  void* Nf;   // [chunks][Hv][4 x token blocks]            N = M (I+A)^-1
+  void* Uf;   // [chunks][Hv][state tiles x token blocks]  U = K^T W (I+A)^-1 diag(beta)
+  void* Nf;   // [chunks][Hv][4 x token blocks]            N = M (I+A)^-1 diag(beta)
   void* Ucf;  // [Hv][state tiles x token blocks]  U weighted for the capture token
   float* sc;  // [chunks][Hv][4][64]  beta, exp(gam), gam, 0
 };
