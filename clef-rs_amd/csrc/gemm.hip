@@ -260,6 +260,7 @@ int launch_epi(const GemmParams& p, hipStream_t s) {
 }  // namespace
 
 int gemm_launch(const GemmParams& p, int epilogue, hipStream_t s) {
+  if (gemm_f16_dma_ok(p)) return gemm_f16_dma_launch(p, epilogue, s);
   if (p.dtype_in == 1) {
     if (epilogue == 0) return launch_epi<half_t, 0>(p, s);
     if (epilogue == 1) return launch_epi<half_t, 1>(p, s);

@@ -20,4 +20,8 @@ struct GemmParams {
 // epilogue: 0 store, 1 residual add into f32 y, 2 SwiGLU
 int gemm_launch(const GemmParams& p, int epilogue, hipStream_t stream);
 
+// f16 large-M path (gemm_f16.hip)
+bool gemm_f16_dma_ok(const GemmParams& p);
+int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t stream);
+
 }  // namespace clef

@@ -1,0 +1,217 @@
+// f16 projection GEMM for large row counts: y = x . W^T, x [M,K], W [N,K]
+// (both K-contiguous), f32 accumulation.  Same contract and epilogues as
+// gemm.hip (neural.metal:7-125 tile GEMM, projection.rs:82-95); selected for
+// M >= 256, K % 64 == 0 and 16-byte aligned rows.
+//
+// A work-group of VM x 2 waves computes a 256 x BN tile, each wave 256/VM x
+// BN/2 with v_mfma_f32_32x32x16_f16 (256 x 256: 2 x 2 waves, one per SIMD,
+// 128 x 128 each with the accumulators in AGPRs; 256 x 128: 4 x 2 waves, two
+// per SIMD, 64 x 64 each).  K advances in 64-element stages through
+// two LDS buffers filled by global->LDS DMA (global_load_lds_dwordx4, 1 KiB
+// per wave instruction): while a stage is multiplied the next one lands.
+// Rows are 128 bytes; the 16-byte chunk c of row r is stored at slot
+// c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit 16
+// distinct bank groups.  The DMA lanes pick their source chunk so that the
+// lane-ordered LDS writes produce that layout.
+#include "common.hpp"
+#include "gemm.hpp"
+
+namespace clef {
+namespace {
+
+constexpr int kBM = 256, kBK = 64;
+
+__device__ __forceinline__ void dma16(const void* src_lane, void* lds_block) {
+  __builtin_amdgcn_global_load_lds(src_lane, lds_block, 16, 0, 0);
+}
+
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
+
+template <int BN, int VM, int EPI>
+__global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
+  constexpr int kWaves = VM * 2;
+  constexpr int WM = kBM / VM, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int NA = kBM * 8 / 64 / kWaves;  // A DMA instructions per wave per stage
+  constexpr int NB = BN * 8 / 64 / kWaves;
+  typedef half8 frag;
+
+  __shared__ __attribute__((aligned(1024))) half_t sA0[kBM * kBK];
+  __shared__ __attribute__((aligned(1024))) half_t sA1[kBM * kBK];
+  __shared__ __attribute__((aligned(1024))) half_t sB0[BN * kBK];
+  __shared__ __attribute__((aligned(1024))) half_t sB1[BN * kBK];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- tile index with XCD-compact placement (as gemm.hip)
+  const int tiles_m = (p.M + kBM - 1) / kBM;
+  const int tiles_n = (EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN);
+  const int ntiles = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+  const int group = 4;
+  const int gsize = group * tiles_n;
+  const int gid = t / gsize;
+  const int first_m = gid * group;
+  const int gm = min(group, tiles_m - first_m);
+  const int tm = first_m + (t % gsize) % gm;
+  const int tn = (t % gsize) / gm;
+  const int m0 = tm * kBM;
+  const int n0 = tn * (EPI == 2 ? BN / 2 : BN);
+
+  const half_t* X = static_cast<const half_t*>(p.x);
+  const half_t* W = static_cast<const half_t*>(p.w);
+  const half_t* W2 = static_cast<const half_t*>(p.w2);
+
+  // ---- DMA sources.  Instruction q of this wave fills LDS slots
+  // [64 j, 64 j + 64) with j = wave * N + q: lane l writes slot 64 j + l, i.e.
+  // row 8 j + l / 8 with swizzled chunk l % 8.  The row's swizzle key
+  // ((8 j + l / 8) >> 1) & 7 = (4 j + l / 16) & 7 depends on j only through
+  // its parity, so a lane needs two column offsets; the row offsets are
+  // uniform.  (Element offsets fit 32 bits: checked by gemm_f16_dma_ok.)
+  int lcol[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
+  const int lrow = lane >> 3;
+  auto issue = [&](half_t* sa, half_t* sb, int k0) {
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      const int j = wave * NA + q;
+      const int row = min(m0 + 8 * j + lrow, p.M - 1);
+      dma16(X + row * (int)p.ldx + lcol[j & 1] + k0, sa + j * 512);
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int j = wave * NB + q;
+      const int row = 8 * j + lrow;
+      const half_t* src;
+      if (EPI == 2) {  // wave column wb holds [gate | up] rows of the same outputs
+        const int wb = row / WN, within = row % WN;
+        const int nr = min(n0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
+        src = (within >= WN / 2 ? W2 : W) + (int64_t)nr * p.ldw;
+      } else {
+        src = W + (int64_t)min(n0 + row, p.N - 1) * p.ldw;
+      }
+      dma16(src + lcol[j & 1] + k0, sb + j * 512);
+    }
+  };
+
+  float16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // fragment reads: row r = (wave offset) + 32 i + lane % 32 has swizzle key
+  // (lane % 32 >> 1) & 7, so a lane's byte offset within any 32-row block is
+  // one of four values (k-block kb); the block offsets are immediates
+  const int frow = lane & 31, fkc = lane >> 5;
+  int foff[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) foff[kb] = 2 * (frow * kBK + (((2 * kb + fkc) ^ ((frow >> 1) & 7)) << 3));
+  auto compute = [&](const half_t* sa, const half_t* sb) {
+    const char* ab = reinterpret_cast<const char*>(sa) + wm * WM * kBK * 2;
+    const char* bb = reinterpret_cast<const char*>(sb) + wn * WN * kBK * 2;
+#pragma unroll
+    for (int kb = 0; kb < kBK / 16; ++kb) {
+      frag af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const frag*>(ab + foff[kb] + i * 32 * kBK * 2);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const frag*>(bb + foff[kb] + j * 32 * kBK * 2);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int nk = p.K / kBK;
+  issue(sA0, sB0, 0);
+  vm_wait_all();
+  lds_barrier();
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool odd = kt & 1;
+    if (kt + 1 < nk) issue(odd ? sA0 : sA1, odd ? sB0 : sB1, (kt + 1) * kBK);
+    compute(odd ? sA1 : sA0, odd ? sB1 : sB0);
+    vm_wait_all();
+    lds_barrier();
+  }
+
+  // ---- epilogue.  acc[i][j][e]: row (e/4)*8 + (lane/32)*4 + e%4, col lane%32
+  const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+  if (EPI == 2) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN / 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
+          const int c = n0 + wn * (WN / 2) + j * 32 + ccol;
+          if (r < p.M && c < p.N) {
+            // half roundings of neural.metal:35-42
+            const float g = static_cast<float>(static_cast<half_t>(acc[i][j][e]));
+            const float s = static_cast<float>(static_cast<half_t>(g / (1.0f + expf(-g))));
+            const float out = s * static_cast<float>(static_cast<half_t>(acc[i][j + TN / 2][e]));
+            static_cast<half_t*>(p.y)[(int64_t)r * p.ldy + c] = static_cast<half_t>(out);
+          }
+        }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
+        const int c = n0 + wn * WN + j * 32 + ccol;
+        if (r < p.M && c < p.N) {
+          const int64_t o = (int64_t)r * p.ldy + c;
+          const float v = acc[i][j][e];
+          if (EPI == 1) {
+            float* y = static_cast<float*>(p.y);
+            y[o] = y[o] + (p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(v)) : v);
+          } else if (p.dtype_out == 1) {
+            static_cast<half_t*>(p.y)[o] = static_cast<half_t>(v);
+          } else {
+            static_cast<float*>(p.y)[o] = v;
+          }
+        }
+      }
+}
+
+template <int BN, int EPI>
+int launch(const GemmParams& p, hipStream_t s) {
+  constexpr int VM = 4;
+  const int tiles_m = (p.M + kBM - 1) / kBM;
+  const int tiles_n = EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_f16_dma<BN, VM, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
+  return check_launch("gemm");
+}
+
+}  // namespace
+
+bool gemm_f16_dma_ok(const GemmParams& p) {
+  return p.dtype_in == 1 && p.vec && p.M >= kBM && p.K % kBK == 0 &&
+         (int64_t)p.M * p.ldx < (int64_t(1) << 31);
+}
+
+// 256 x 256 tiles unless that leaves most of the 256 CUs idle
+int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t s) {
+  const int n_eff = epilogue == 2 ? 2 * p.N : p.N;
+  const long tiles256 = (long)((p.M + kBM - 1) / kBM) * ((n_eff + 255) / 256);
+  const bool wide = tiles256 >= 384;
+  if (epilogue == 0) return wide ? launch<256, 0>(p, s) : launch<128, 0>(p, s);
+  if (epilogue == 1) return wide ? launch<256, 1>(p, s) : launch<128, 1>(p, s);
+  return wide ? launch<256, 2>(p, s) : launch<128, 2>(p, s);
+}
+
+}  // namespace clef
