@@ -3,12 +3,12 @@
 // gemm.hip (neural.metal:7-125 tile GEMM, projection.rs:82-95); selected for
 // M >= 256, K % 64 == 0 and 16-byte aligned rows.
 //
-// A work-group of VM x 2 waves computes a 256 x BN tile, each wave 256/VM x
-// BN/2 with v_mfma_f32_32x32x16_f16 (256 x 256: 2 x 2 waves, one per SIMD,
-// 128 x 128 each with the accumulators in AGPRs; 256 x 128: 4 x 2 waves, two
-// per SIMD, 64 x 64 each).  K advances in 64-element stages through
-// two LDS buffers filled by global->LDS DMA (global_load_lds_dwordx4, 1 KiB
-// per wave instruction): while a stage is multiplied the next one lands.
+// A work-group of 8 waves (4 x 2, two per SIMD) computes a 256 x BN tile,
+// each wave 64 x BN/2 with v_mfma_f32_32x32x16_f16 (at most 128 accumulator
+// registers per wave, which the register allocator keeps in place).  K
+// advances in 64-element stages through two LDS buffers filled by
+// global->LDS DMA (global_load_lds_dwordx4, 1 KiB per wave instruction):
+// while a stage is multiplied the next one lands.
 // Rows are 128 bytes; the 16-byte chunk c of row r is stored at slot
 // c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit 16
 // distinct bank groups.  The DMA lanes pick their source chunk so that the
@@ -21,14 +21,26 @@ namespace {
 
 constexpr int kBM = 256, kBK = 64;
 
+// global_load_lds_dwordx4 written as inline asm: the compiler does not see an
+// LDS write it would have to order before every later LDS read (it would
+// wait for all DMAs in flight, i.e. for the next stage, before computing on
+// the current one).  Completion is awaited explicitly (vmcnt) before the
+// barrier that publishes a stage.  The LDS destination goes in M0 (low 32
+// bits of the LDS address); lane l writes 16 bytes at M0 + 16 l.
 __device__ __forceinline__ void dma16(const void* src_lane, void* lds_block) {
-  __builtin_amdgcn_global_load_lds(src_lane, lds_block, 16, 0, 0);
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_block));
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src_lane), "{m0}"(m0) : "memory");
 }
 
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+template <int N>
+__device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N)
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 
-template <int BN, int VM, int EPI>
+template <int BN, int VM, int NS, int EPI>
 __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int kWaves = VM * 2;
   constexpr int WM = kBM / VM, WN = BN / 2;
@@ -37,10 +49,8 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int NB = BN * 8 / 64 / kWaves;
   typedef half8 frag;
 
-  __shared__ __attribute__((aligned(1024))) half_t sA0[kBM * kBK];
-  __shared__ __attribute__((aligned(1024))) half_t sA1[kBM * kBK];
-  __shared__ __attribute__((aligned(1024))) half_t sB0[BN * kBK];
-  __shared__ __attribute__((aligned(1024))) half_t sB1[BN * kBK];
+  __shared__ __attribute__((aligned(1024))) half_t sA[NS][kBM * kBK];
+  __shared__ __attribute__((aligned(1024))) half_t sB[NS][BN * kBK];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -114,34 +124,54 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   int foff[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) foff[kb] = 2 * (frow * kBK + (((2 * kb + fkc) ^ ((frow >> 1) & 7)) << 3));
+  // k-block kb+1's fragments are requested before kb's products
   auto compute = [&](const half_t* sa, const half_t* sb) {
     const char* ab = reinterpret_cast<const char*>(sa) + wm * WM * kBK * 2;
     const char* bb = reinterpret_cast<const char*>(sb) + wn * WN * kBK * 2;
+    frag af[2][TM], bf[2][TN];
+    auto load = [&](int kb) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[kb & 1][i] = *reinterpret_cast<const frag*>(ab + foff[kb] + i * 32 * kBK * 2);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[kb & 1][j] = *reinterpret_cast<const frag*>(bb + foff[kb] + j * 32 * kBK * 2);
+    };
+    load(0);
 #pragma unroll
     for (int kb = 0; kb < kBK / 16; ++kb) {
-      frag af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const frag*>(ab + foff[kb] + i * 32 * kBK * 2);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const frag*>(bb + foff[kb] + j * 32 * kBK * 2);
+      if (kb + 1 < kBK / 16) load(kb + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kb & 1][i], bf[kb & 1][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
+  // NS-stage ring: stage kt+NS-1 is requested while stage kt is multiplied;
+  // each wave then waits for its own requests of stage kt+1 (the newest
+  // NS-2 stages may stay in flight) before the barrier that publishes it.
   const int nk = p.K / kBK;
-  issue(sA0, sB0, 0);
-  vm_wait_all();
-  lds_barrier();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool odd = kt & 1;
-    if (kt + 1 < nk) issue(odd ? sA0 : sA1, odd ? sB0 : sB1, (kt + 1) * kBK);
-    compute(odd ? sA1 : sA0, odd ? sB1 : sB0);
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < nk) issue(sA[st], sB[st], st * kBK);
+  if (NS == 3 && nk > 1)
+    vm_wait<NA + NB>();
+  else
     vm_wait_all();
+  lds_barrier();
+  int cur = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int nxt = cur + NS - 1 >= NS ? cur - 1 : cur + NS - 1;  // (cur + NS - 1) % NS
+    const bool more = kt + NS - 1 < nk;
+    if (more) issue(sA[nxt], sB[nxt], (kt + NS - 1) * kBK);
+    compute(sA[cur], sB[cur]);
+    if (NS == 3 && more)
+      vm_wait<NA + NB>();
+    else
+      vm_wait_all();
     lds_barrier();
+    cur = cur + 1 == NS ? 0 : cur + 1;
   }
 
   // ---- epilogue.  acc[i][j][e]: row (e/4)*8 + (lane/32)*4 + e%4, col lane%32
@@ -191,9 +221,10 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
 template <int BN, int EPI>
 int launch(const GemmParams& p, hipStream_t s) {
   constexpr int VM = 4;
+  constexpr int NS = 2;
   const int tiles_m = (p.M + kBM - 1) / kBM;
   const int tiles_n = EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_f16_dma<BN, VM, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
+  hipLaunchKernelGGL((gemm_f16_dma<BN, VM, NS, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
   return check_launch("gemm");
 }
 
