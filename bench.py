@@ -40,7 +40,23 @@ def parse():
     ap.add_argument("--cpu-tokens", type=int, default=1024,
                     help="tokens of the bounded CPU-oracle sample (0 disables it)")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run one plain device copy of this many MiB (the known-size reference for "
+                         "HBM byte counters under rocprofv3 --pmc)")
     return ap.parse_args()
+
+
+def measured_traffic(T, profile):
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy of known size), or
+    None when no summary matches this workload."""
+    path = ROOT / "profiles" / f"gemm_traffic_T{T}_{profile}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(float(line.split("=")[1]))
+    return None
 
 
 def event_ms(fn, steps, warmup, torch):
@@ -102,6 +118,12 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     T = args.tokens
     cfg = workloads.block_config()
     weights = workloads.block_weights(cfg, seed=3, device=dev)
@@ -156,13 +178,13 @@ def main():
             "tokens": T, "global_batch": 1, "seq_len": T, "layers": 4,
         },
         "roofline": {
-            "kernel": "projection GEMMs (gemm_kernel, all launches of a step)",
+            "kernel": "projection GEMMs (gemm_f16_dma / gemm_kernel, all launches of a step)",
             "bound": "mfma",
             "achieved": round(gemm_tfs, 2),
             "peak": MFMA_PEAK_TFS[dt],
             "unit": "TFLOP/s",
             "frac": round(gemm_tfs / MFMA_PEAK_TFS[dt], 4),
-            "traffic": None,
+            "traffic": measured_traffic(T, args.profile),
         },
         "scan": {
             "in_block_GBs": round(scan_gbs, 1),

@@ -47,11 +47,20 @@ SIGNATURES = {
     "clef_delta_scan_workspace": (_z, [_i] * 7),
     "clef_delta_scan": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _i, _i, _i,
                              _p, _i, _p, _l, _i, _p, _p, _p, _z, _p]),
+    "clef_delta_scan_varlen_workspace": (_z, [_i] * 8),
+    "clef_delta_scan_varlen": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i,
+                                    _p, _l, _p, _l, _i, _p, _p, _z, _p]),
     "clef_gemm": (_i, [_p, _l, _p, _l, _p, _l, _i, _i, _i, _i, _i, _i, _p]),
     "clef_gemm_swiglu": (_i, [_p, _l, _p, _p, _l, _p, _l, _i, _i, _i, _i, _p]),
     "clef_rms_norm": (_i, [_p, _l, _i, _p, _p, _l, _i, _i, _i, _f, _p]),
     "clef_conv_silu": (_i, [_p, _l, _i, _p, _i, _p, _i, _p, _l, _i, _i, _i, _p]),
     "clef_delta_gates": (_i, [_p, _l, _p, _l, _i, _p, _p, _p, _p, _i, _i, _p]),
+    "clef_attention_varlen_workspace": (_z, [_i, _i]),
+    "clef_attention_gated_varlen": (_i, [_p, _l, _p, _l, _p, _l, _p, _i, _i, _p, _l, _p, _l, _i, _i, _i, _i, _i,
+                                         _p, _l, _l, _p, _l, _p, _z, _p]),
+    "clef_conv_silu_varlen": (_i, [_p, _l, _i, _p, _i, _l, _p, _i, _p, _i, _p, _l, _i, _i, _i, _p]),
+    "clef_qk_norm_rotary_varlen": (_i, [_p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _d, _i, _p, _i, _i, _f,
+                                        _p]),
     "clef_gated_rms_silu": (_i, [_p, _p, _l, _i, _p, _p, _i, _i, _i, _i, _f, _p]),
     "clef_qk_norm_rotary": (_i, [_p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _d, _i, _i, _f, _p]),
     "clef_values_transposed": (_i, [_p, _l, _i, _p, _l, _i, _i, _i, _i, _i, _p]),
@@ -169,6 +178,51 @@ class DeltaScan:
             _ptr(out), so, _dt(out), _ptr(captured), _ptr(final), _ptr(ws), ws.numel(), _stream()))
         return out, captured, final
 
+    def prefill_varlen(self, q, k, v, g, beta, cu_seqlens, initial=None, out_dtype=torch.float32,
+                       want_final=True, out=None):
+        """Ragged batch: tokens cu_seqlens[s]..cu_seqlens[s+1]-1 form sequence s.
+
+        cu_seqlens: int32 device tensor [nseq + 1].  initial: None, one shared
+        [Hv, dk, dv] state, or [nseq, Hv, dk, dv] per-sequence states (f32).
+        Returns (out [T, Hv, dv], final [nseq, Hv, dk, dv] or None).
+        """
+        T, Hk, dk = q.shape
+        Hv, dv = v.shape[1], v.shape[2]
+        nseq = cu_seqlens.numel() - 1
+        if k.shape != q.shape or v.shape[0] != T or dk != self.key_dim or dv != self.value_dim:
+            raise ClefError(-1, "DeltaNet tensor shapes")
+        if g.shape != (T, Hv) or beta.shape != (T, Hv) or g.dtype != beta.dtype or g.stride(0) != beta.stride(0):
+            raise ClefError(-1, "DeltaNet gate shapes")
+        if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_cuda or not cu_seqlens.is_contiguous():
+            raise ClefError(-1, "cu_seqlens must be a contiguous int32 device tensor")
+        sqk = _token_view(q, "q", 2)
+        _token_view(k, "k", 2)
+        sv = _token_view(v, "v", 2)
+        dev = q.device
+        if out is None:
+            out = torch.empty((T, Hv, dv), dtype=out_dtype, device=dev)
+        so = _token_view(out, "out", 2)
+        stride = 0
+        if initial is not None:
+            if initial.dtype != torch.float32 or not initial.is_contiguous():
+                raise ClefError(-1, "initial states must be contiguous f32")
+            if initial.shape == (nseq, Hv, dk, dv):
+                stride = Hv * dk * dv
+            elif initial.shape != (Hv, dk, dv):
+                raise ClefError(-1, "initial state must be [Hv, dk, dv] or [nseq, Hv, dk, dv]")
+        final = torch.empty((nseq, Hv, dk, dv), dtype=torch.float32, device=dev) if want_final else None
+        n = lib().clef_delta_scan_varlen_workspace(T, nseq, Hk, Hv, dk, dv, self.chunk, self.precision)
+        if n == 0:
+            raise ClefError(-1, last_error())
+        ws = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+        off = (-ws.data_ptr()) % 256
+        ws = ws[off:off + n]
+        _check(lib().clef_delta_scan_varlen(
+            _ptr(q), _ptr(k), _ptr(v), sqk, sv, _dt(q), _ptr(g), _ptr(beta), g.stride(0), _dt(g),
+            _ptr(cu_seqlens), nseq, T, Hk, Hv, dk, dv, self.chunk, self.precision, _ptr(initial), stride,
+            _ptr(out), so, _dt(out), _ptr(final), _ptr(ws), ws.numel(), _stream()))
+        return out, final
+
 
 def _rows(t, name):
     if t.dim() != 2 or t.stride(1) != 1 or not t.is_cuda:
@@ -234,6 +288,23 @@ def conv_silu(x, w, history=None, out_dtype=torch.float32):
     return y
 
 
+def conv_silu_varlen(x, w, cu_seqlens, history=None, out_dtype=torch.float32):
+    """Ragged batch: history None, one [rows, W] history shared by every sequence,
+    or [nseq, rows, W] per sequence (f32)."""
+    T, W = x.shape
+    taps = w.reshape(W, -1).shape[1]
+    nseq = cu_seqlens.numel() - 1
+    y = torch.empty((T, W), dtype=out_dtype, device=x.device)
+    rows, stride = 0, 0
+    if history is not None:
+        rows = history.shape[-2]
+        stride = rows * W if history.dim() == 3 else 0
+    _check(lib().clef_conv_silu_varlen(_ptr(x), _rows(x, "x"), _dt(x), _ptr(history), rows, stride,
+                                       _ptr(cu_seqlens), nseq, _ptr(w.reshape(W, taps).contiguous()), taps,
+                                       _ptr(y), W, _dt(y), T, W, _stream()))
+    return y
+
+
 def delta_gates(a, b, dt, a_log):
     T, Hv = a.shape
     g = torch.empty((T, Hv), dtype=torch.float32, device=a.device)
@@ -263,6 +334,17 @@ def qk_norm_rotary(x, heads, d, w, rot_dim, theta, pos0=0, head_stride=None, eps
     return out
 
 
+def qk_norm_rotary_varlen(x, heads, d, w, rot_dim, theta, cu_seqlens, pos0=0, head_stride=None, eps=1e-6,
+                          out_dtype=None):
+    T = x.shape[0]
+    hs = head_stride or d
+    out = torch.empty((heads, T, d), dtype=out_dtype or x.dtype, device=x.device)
+    _check(lib().clef_qk_norm_rotary_varlen(_ptr(x), x.stride(0), hs, _dt(x), _ptr(w), _ptr(out), T, _dt(out), T,
+                                            heads, d, rot_dim, float(theta), pos0, _ptr(cu_seqlens),
+                                            cu_seqlens.numel() - 1, 0, float(eps), _stream()))
+    return out
+
+
 def values_transposed(x, heads, d, ld_tok=None, out=None, dst_offset=0, out_dtype=None):
     T = x.shape[0]
     if out is None:
@@ -282,6 +364,27 @@ def attention_gated(q, k, vt, gate, kn=None):
     _check(lib().clef_attention_gated(_ptr(q), qn, _ptr(k), kn_, _ptr(vt), vt.shape[2], _dt(q), heads, kvh,
                                       qn, kn, d, _ptr(gate), gate.stride(0), gate.stride(1), _ptr(y),
                                       heads * d, _stream()))
+    return y
+
+
+def attention_gated_varlen(q, k, vt, gate, cu_seqlens, prefix_k=None, prefix_vt=None):
+    """Ragged batch: q [heads, T, d], k [kvh, T, d], vt [kvh, d, ldv] packed by
+    cu_seqlens (int32 device); optional shared prefix keys [kvh, np, d] and
+    values^T [kvh, d, ldpv] visible to every query."""
+    heads, T, d = q.shape
+    kvh = k.shape[0]
+    nseq = cu_seqlens.numel() - 1
+    y = torch.empty((T, heads * d), dtype=q.dtype, device=q.device)
+    np_ = 0 if prefix_k is None else prefix_k.shape[1]
+    n = lib().clef_attention_varlen_workspace(T, nseq)
+    ws = torch.empty(n + 256, dtype=torch.uint8, device=q.device)
+    off = (-ws.data_ptr()) % 256
+    ws = ws[off:off + n]
+    _check(lib().clef_attention_gated_varlen(
+        _ptr(q), T, _ptr(k), k.shape[1], _ptr(vt), vt.shape[2], _ptr(cu_seqlens), nseq, T,
+        _ptr(prefix_k), np_, _ptr(prefix_vt), 0 if prefix_vt is None else prefix_vt.shape[2], np_, _dt(q),
+        heads, kvh, d, _ptr(gate), gate.stride(0), gate.stride(1), _ptr(y), heads * d, _ptr(ws), ws.numel(),
+        _stream()))
     return y
 
 
@@ -311,6 +414,9 @@ SIGNATURES.update({
     "clef_backbone_workspace": (_z, [_p, _i, _i]),
     "clef_backbone_prefix_bytes": (_z, [_p, _i]),
     "clef_backbone_prefill": (_i, [_p, C.POINTER(C.c_int32), _i, _p, _i, _i, _p, _p, _p, _z, _p]),
+    "clef_backbone_varlen_workspace": (_z, [_p, _i, _i, _i]),
+    "clef_backbone_prefill_varlen": (_i, [_p, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _i, _p, _i, _p, _p, _z,
+                                          _p]),
     "clef_backbone_enable_timing": (_i, [_p, _i]),
     "clef_backbone_timings": (_i, [_p, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double),
                                    C.POINTER(C.c_double)]),
@@ -456,6 +562,29 @@ class Backbone:
             _ptr(saved.buffer) if saved is not None else None, _ptr(hidden), _ptr(ws), ws.numel(),
             _stream()))
         return hidden, saved
+
+    def prefill_varlen(self, ids, cu_seqlens, initial: PrefixState = None, hidden=None):
+        """Ragged batch of requests resumed from one shared prefix: ids packed
+        by cu_seqlens (host int arrays).  Returns hidden f32 [T, H] (no prefix
+        rows); sequence s's rows equal prefill(ids[cu[s]:cu[s+1]], initial)."""
+        import numpy as np
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
+        T, nseq = int(ids.shape[0]), int(cu.shape[0]) - 1
+        prefix = initial.tokens if initial is not None else 0
+        dev = torch.device("cuda", torch.cuda.current_device())
+        if hidden is None:
+            hidden = torch.empty((T, self.c.hidden), dtype=torch.float32, device=dev)
+        n = lib().clef_backbone_varlen_workspace(self._h, T, nseq, prefix)
+        if n == 0:
+            raise ClefError(-1, "prefill: ragged batch dimensions")
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = torch.empty(n, dtype=torch.uint8, device=dev)
+        _check(lib().clef_backbone_prefill_varlen(
+            self._h, ids.ctypes.data_as(C.POINTER(C.c_int32)), cu.ctypes.data_as(C.POINTER(C.c_int32)), nseq,
+            _ptr(initial.buffer) if initial is not None else None, prefix, _ptr(hidden), _ptr(self._ws),
+            self._ws.numel(), _stream()))
+        return hidden
 
 
 def head_logits(x_row, w):

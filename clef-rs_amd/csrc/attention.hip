@@ -1,7 +1,8 @@
 // Gated causal GQA attention for the full-attention layer (qwen.rs:451-525),
 // with the online softmax of ops.rs:62-148 and the sigmoid gate of
 // qwen.rs:518-524.  Replaces the reference's Metal flash-attention op
-// (metal.rs:415-633).
+// (metal.rs:415-633).  This file holds the entry point and the f32 kernel
+// (also used for f16 shapes attention_f16.hip does not take).
 //
 // One work-group (4 waves) owns 64 query rows of one head; each wave owns 16
 // rows.  Key tiles of 64 are staged in LDS as K [key][d] and V^T [d][key]
@@ -15,21 +16,11 @@
 #include <cmath>
 
 #include "../../include/clef_hip.h"
+#include "attention.hpp"
 #include "common.hpp"
 
 namespace clef {
 namespace {
-
-struct AttnParams {
-  const void* q;
-  const void* k;
-  const void* vt;
-  const void* gate;
-  void* y;
-  int64_t ldq, ldk, ldv, ldg, hsg, ldy;
-  int heads, kvh, qn, kn, d;
-  float scale;
-};
 
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
@@ -232,6 +223,50 @@ extern "C" int clef_attention_gated(const void* q, int64_t ldq_tok, const void* 
                "attention: gate or output strides");
   clef::AttnParams p{q, k, vt, gate, y, ldq_tok, ldk_tok, ldv_tok, ldg, hsg, ldy, heads, kv_heads, qn, kn, d,
                      static_cast<float>(1.0 / std::sqrt(static_cast<double>(d)))};
-  if (dtype == CLEF_F16) return clef::launch_d<clef::half_t>(p, static_cast<hipStream_t>(stream));
+  if (dtype == CLEF_F16) {
+    if (clef::attn_f16_ok(p)) return clef::attn_f16_launch(p, static_cast<hipStream_t>(stream));
+    return clef::launch_d<clef::half_t>(p, static_cast<hipStream_t>(stream));
+  }
   return clef::launch_d<float>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t clef_attention_varlen_workspace(int T, int nseq) {
+  if (T < 1 || nseq < 1 || nseq > 4096) return 0;
+  return clef::attn_tables_bytes(T, nseq);
+}
+
+extern "C" int clef_attention_gated_varlen(const void* q, int64_t ldq_tok, const void* k, int64_t ldk_tok,
+                                           const void* vt, int64_t ldv_tok, const int32_t* cu_seqlens, int nseq,
+                                           int T, const void* prefix_k, int64_t ldpk_tok, const void* prefix_vt,
+                                           int64_t ldpv_tok, int np, int dtype, int heads, int kv_heads, int d,
+                                           const void* gate, int64_t ldg, int64_t hsg, void* y, int64_t ldy,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+  CLEF_REQUIRE(q && k && vt && gate && y && cu_seqlens && workspace, "attention: null pointer");
+  CLEF_REQUIRE(dtype == CLEF_F16, "attention: ragged batches run in the mixed profile (f16)");
+  CLEF_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "attention: head counts");
+  CLEF_REQUIRE(T >= 1 && nseq >= 1 && nseq <= 4096, "attention: 1 <= T and 1 <= nseq <= 4096");
+  CLEF_REQUIRE(d >= 8 && d <= 256 && d % 8 == 0, "attention: head width must be a multiple of 8 in 8..256");
+  CLEF_REQUIRE(ldq_tok >= T && ldk_tok >= T && ldv_tok >= T && ldv_tok % 8 == 0 && ldv_tok >= 64,
+               "attention: token strides (ldv_tok must be >= 64 and a multiple of 8)");
+  CLEF_REQUIRE(np >= 0 && np % 8 == 0 && (np == 0 || (prefix_k && prefix_vt && ldpk_tok >= np && ldpv_tok >= np)),
+               "attention: prefix keys (np % 8 == 0, buffers and strides)");
+  CLEF_REQUIRE(hsg >= d && ldg >= (int64_t)(heads - 1) * hsg + d && ldy >= (int64_t)heads * d,
+               "attention: gate or output strides");
+  CLEF_REQUIRE(workspace_bytes >= clef::attn_tables_bytes(T, nseq) &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+               "attention: workspace too small or not 256-byte aligned");
+  clef::AttnParams p{q, k, vt, gate, y, ldq_tok, ldk_tok, ldv_tok, ldg, hsg, ldy, heads, kv_heads, T, 0, d,
+                     static_cast<float>(1.0 / std::sqrt(static_cast<double>(d)))};
+  CLEF_REQUIRE(clef::attn_f16_ok(p), "attention: strides beyond the 32-bit offsets of the f16 kernel");
+  p.cu_q = cu_seqlens;
+  p.nseq = nseq;
+  p.pk = prefix_k;
+  p.pvt = prefix_vt;
+  p.ldpk = ldpk_tok;
+  p.ldpv = ldpv_tok;
+  p.np = np;
+  clef::attn_carve_tables(p, workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (int rc = clef::attn_f16_tables(p, st)) return rc;
+  return clef::attn_f16_launch(p, st);
 }

@@ -1,0 +1,42 @@
+// Internal launch interface of the gated causal attention core.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace clef {
+
+struct AttnParams {
+  const void* q;     // [heads][ldq][d]
+  const void* k;     // [kvh][ldk][d]
+  const void* vt;    // [kvh][d][ldv]  (values transposed: keys contiguous)
+  const void* gate;  // gate of (token, head, e) at token * ldg + head * hsg + e
+  void* y;           // [qn][ldy], head h at columns h * d ..
+  int64_t ldq, ldk, ldv, ldg, hsg, ldy;
+  int heads, kvh, qn, kn, d;
+  float scale;
+  // Ragged batch (cu_q non-null; qn = packed tokens T, kn unused): sequence s
+  // owns rows cu_q[s] .. cu_q[s+1]-1 of q, k, vt, gate and y, and its queries
+  // see the np prefix keys (pk, pvt; all visible) before its own, causally.
+  const int* cu_q;   // [nseq + 1] (device)
+  int2* pairs;       // [blocks / heads] {sequence, query tile}, most keys first
+  int* npairs;       // valid entries of pairs
+  int nseq;
+  const void* pk;    // [kvh][ldpk][d] or null
+  const void* pvt;   // [kvh][d][ldpv]
+  int64_t ldpk, ldpv;
+  int np;
+  int vec_io;        // set at launch: gate and y rows allow 8-byte accesses
+};
+
+// device tables of a ragged batch (workspace: attn_tables_bytes)
+size_t attn_tables_bytes(int T, int nseq);
+void attn_carve_tables(AttnParams& p, void* ws);
+int attn_f16_tables(const AttnParams& p, hipStream_t s);
+
+// f16 flash-attention path (MFMA 32x32x16, LDS-DMA key/value tiles); false if
+// the shape is outside what it handles, in which case nothing is launched.
+bool attn_f16_ok(const AttnParams& p);
+int attn_f16_launch(const AttnParams& p, hipStream_t s);
+
+}  // namespace clef

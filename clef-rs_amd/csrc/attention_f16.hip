@@ -1,0 +1,536 @@
+// f16 gated causal GQA attention core (qwen.rs:451-525 with the online
+// softmax of ops.rs:62-148), the mixed-profile path of clef_attention_gated.
+//
+// A work-group of 4 waves owns 128 queries of one head; wave w owns queries
+// q0 + 32 w + (0..31).  Keys advance in tiles of 64, staged in LDS by
+// global->LDS DMA (K as [key][d], V^T as [d][key]) one tile ahead.
+//
+// The scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_f16:
+// the accumulator of a 32-key x 32-query tile leaves lane l one query
+// (l % 32) and 16 keys, so each lane does its own query's softmax over its
+// keys and combines with one partner lane (l ^ 32) for the row maximum and
+// sum.  Key rows are stored in LDS in the order pi(r) = r with bits 2 and 3
+// swapped; with that order the 16 probabilities a lane holds are exactly its
+// B-operand fragments of O^T = V^T P^T for two 16-key blocks in natural key
+// order, so P never leaves registers.  The output accumulator O^T likewise
+// gives each lane one query, so the softmax rescale is a per-lane factor.
+//
+// Rescaling is lazy: the running reference maximum only moves (and O and the
+// row sum are rescaled) when the new maximum exceeds it by more than 8 in
+// log2 units; otherwise the probabilities exp2((s - m_ref) c) stay below
+// 2^8.  Both O and the row sum use the same reference, so O / l is the
+// softmax average exactly as in the eager formulation.
+#include "attention.hpp"
+#include "common.hpp"
+
+namespace clef {
+namespace {
+
+// global_load_lds_dwordx4 as inline asm (see gemm_f16.hip): lane l writes 16
+// bytes at M0 + 16 l; completion is awaited with an explicit vmcnt wait.
+// dma16 takes a per-lane address, dma16s a wave-uniform base plus a per-lane
+// 32-bit byte offset (no per-lane address arithmetic).
+// The compiler does not see the load inside the asm, so the asm carries the
+// wait states its operands need: 1 after the SALU write of M0 that precedes
+// an LDS DMA, 5 between a VALU write of an SGPR (the readfirstlane of the
+// base) and a vector-memory read of it.
+__device__ __forceinline__ void dma16(const void* src_lane, void* lds_block) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_block));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, void* lds_block) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_block));
+  // the base is wave-uniform; readfirstlane pins it to SGPRs as the encoding requires
+  // (readfirstlane returns int: each half is widened as unsigned)
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(sb), "{m0}"(m0) : "memory");
+}
+
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
+// combine lane l with lane l ^ 32
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// key order of the LDS key rows within a 64-key tile (an involution)
+__device__ __forceinline__ int key_perm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// XOR key of the 16-byte slots of key row r: rows of 256 bytes or more use
+// 16 keys (one per 16-byte bank group of a 256-byte bank row), 128-byte rows
+// pair up in a bank row and use 8 keys per row pair
+template <int D>
+__device__ __forceinline__ int kswz(int r) { return D >= 128 ? (r & 15) : ((r >> 1) & 7); }
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_f16(AttnParams p) {
+  constexpr int BQ = 128, BK = 64;
+  constexpr int KS = D / 8;       // 16-byte chunks per key row
+  constexpr int NKB = D / 16;     // k-blocks of S^T = K Q^T
+  constexpr int NDT = D / 32;     // 32-row tiles of O^T
+  constexpr int NDMA = D / 32;    // DMA instructions per wave, per operand and tile
+  constexpr int KROWS = 512 / D;  // key rows per 1 KiB DMA instruction
+  constexpr int PD = 8;           // LDS fragment reads in flight ahead of the MFMAs
+  static_assert(D == 64 || D == 128 || D == 256, "head width tile");
+
+  __shared__ __attribute__((aligned(1024))) half_t sK[2][BK * D];
+  __shared__ __attribute__((aligned(1024))) half_t sV[2][D * BK];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, g = lane >> 5;
+
+  // Persistent work-groups (as many as fit on the chip): work items (query
+  // tile, head) are numbered longest first and dealt to the work-groups in
+  // boustrophedon order (b, 2B-1-b, 2B+b, ...), so every work-group gets a
+  // near-equal share of key tiles whatever order the hardware places them in
+  // (it does not hand a waiting work-group to the first CU that frees up).
+  // Within a rank, consecutive items on one XCD get adjacent heads (with
+  // heads % 8 == 0), which share key/value heads and so that XCD's L2.
+  const int nitems = (p.cu_q ? *p.npairs : (p.qn + BQ - 1) / BQ) * p.heads;
+  const int nwg = gridDim.x;
+  for (int round = 0;; ++round) {
+  const int item = round * nwg + ((round & 1) ? nwg - 1 - (int)blockIdx.x : (int)blockIdx.x);
+  if (item >= nitems) break;
+  const int rank = item / p.heads, hi = item % p.heads;
+  const int h = (p.heads & 7) == 0 ? (hi & 7) * (p.heads >> 3) + (hi >> 3) : hi;
+  // this block's sequence: queries qb0 + (0..qn-1); keys 0..na-1 from the
+  // prefix buffers, na..kn-1 from rows kb0 + (0..kn-na-1) of k / vt
+  int q0, qb0 = 0, qn = p.qn, kn = p.kn, na = 0;
+  if (p.cu_q) {
+    const int2 e = p.pairs[rank];
+    const int a = min(max(p.cu_q[e.x], 0), p.qn), b = min(max(p.cu_q[e.x + 1], a), p.qn);
+    qb0 = a;
+    qn = b - a;
+    na = p.np;
+    kn = na + qn;
+    q0 = e.y * BQ;
+  } else {
+    q0 = ((p.qn + BQ - 1) / BQ - 1 - rank) * BQ;
+  }
+  const int kb0 = qb0;
+  const int kvh = h / (p.heads / p.kvh);
+  const int offset = kn - qn;
+  const int d = p.d;
+
+  const half_t* Q = static_cast<const half_t*>(p.q) + (int64_t)h * p.ldq * d + (int64_t)qb0 * d;
+  const half_t* Kb = static_cast<const half_t*>(p.k) + (int64_t)kvh * p.ldk * d + (int64_t)kb0 * d;
+  const half_t* Vb = static_cast<const half_t*>(p.vt) + (int64_t)kvh * d * p.ldv + kb0;
+  const half_t* Kp = p.pk ? static_cast<const half_t*>(p.pk) + (int64_t)kvh * p.ldpk * d : nullptr;
+  const half_t* Vp = p.pvt ? static_cast<const half_t*>(p.pvt) + (int64_t)kvh * d * p.ldpv : nullptr;
+
+  // Q^T fragments (B operand): lane (n, g) holds d = 16 kb + 8 g .. + 7 of its query
+  half8 qf[NKB];
+  {
+    const int r = min(q0 + 32 * wave + n, qn - 1);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int c = 16 * kb + 8 * g;
+      qf[kb] = c < d ? *reinterpret_cast<const half8*>(Q + (int64_t)r * d + c) : half8{};
+    }
+  }
+
+  // ---- DMA sources.  Instruction t = wave * NDMA + q writes 1 KiB: for K,
+  // rows t * KROWS + lane / KS, slot lane % KS holding chunk slot ^ kswz(row)
+  // of key pi(row); for V^T, d-row 8 t + lane / 8, slot lane % 8 holding
+  // keys 8 c .. 8 c + 7 with c = slot ^ ((row >> 1) & 7).  d past the head
+  // width reads in-bounds data that multiplies zero queries (K) or lands in
+  // unstored outputs (V).  Tiles inside [0, kn) use a uniform base and the
+  // per-lane byte offsets ko / vo; the last tile clamps keys to kn - 1 (K,
+  // masked) and ldv - 8 (V, zeroed below).  Ragged batches: tiles inside the
+  // prefix or inside the sequence's own keys take the same fast path from
+  // their segment's base (V prefix tiles excepted: another row stride); the
+  // rest pick each row's segment (na % 8 == 0 keeps 8-key chunks whole).
+  uint32_t ko[NDMA], vo[NDMA];
+  int kr[NDMA];
+#pragma unroll
+  for (int q = 0; q < NDMA; ++q) {
+    const int row = (wave * NDMA + q) * KROWS + lane / KS;
+    kr[q] = key_perm(row);
+    const int kc = 8 * min((lane % KS) ^ kswz<D>(row), d / 8 - 1);
+    ko[q] = 2u * (uint32_t)(kr[q] * d + kc);
+    const int vrow = (wave * NDMA + q) * 8 + (lane >> 3);
+    const int vc = 8 * ((lane & 7) ^ ((vrow >> 1) & 7));
+    vo[q] = 2u * (uint32_t)(min(vrow, d - 1) * (int)p.ldv + vc);
+  }
+  const int kn1 = kn - 1, ldv8 = (int)p.ldv - 8 - kb0;
+  auto issue_k = [&](int buf, int j0) {
+    if (j0 >= na && j0 + BK <= kn) {
+      const half_t* kb = Kb + (int64_t)(j0 - na) * d;
+#pragma unroll
+      for (int q = 0; q < NDMA; ++q) dma16s(kb, ko[q], &sK[buf][(wave * NDMA + q) * 512]);
+    } else if (j0 + BK <= na) {
+      const half_t* kb = Kp + (int64_t)j0 * d;
+#pragma unroll
+      for (int q = 0; q < NDMA; ++q) dma16s(kb, ko[q], &sK[buf][(wave * NDMA + q) * 512]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NDMA; ++q) {
+        const int key = min(j0 + kr[q], kn1);
+        const half_t* row = key < na ? Kp + (int64_t)key * d : Kb + (int64_t)(key - na) * d;
+        const char* src = reinterpret_cast<const char*>(row) + (ko[q] - 2u * (uint32_t)(kr[q] * d));
+        dma16(src, &sK[buf][(wave * NDMA + q) * 512]);
+      }
+    }
+  };
+  auto issue_v = [&](int buf, int j0) {
+    if (j0 >= na && j0 + BK <= kn) {
+      const half_t* vb = Vb + (j0 - na);
+#pragma unroll
+      for (int q = 0; q < NDMA; ++q) dma16s(vb, vo[q], &sV[buf][(wave * NDMA + q) * 512]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NDMA; ++q) {
+        const int vrow = min((wave * NDMA + q) * 8 + (lane >> 3), d - 1);
+        const int c0 = j0 + 8 * ((lane & 7) ^ ((((wave * NDMA + q) * 8 + (lane >> 3)) >> 1) & 7));
+        const half_t* src = c0 < na ? Vp + (int64_t)vrow * p.ldpv + c0
+                                    : Vb + ((int64_t)vrow * p.ldv + min(c0 - na, ldv8));
+        dma16(src, &sV[buf][(wave * NDMA + q) * 512]);
+      }
+    }
+  };
+
+  // ---- fragment read offsets (bytes).  K: row 32 kh + n, chunk 2 kb + g at
+  // slot chunk ^ kswz(n) (kswz(32 kh + n) = kswz(n)); V^T: row 32 dt + n,
+  // chunk 2 kb2 + g at slot chunk ^ ((n >> 1) & 7).  The rest of each address
+  // is an immediate.
+  constexpr int KPER = D >= 128 ? 8 : 4;  // k-blocks per swizzle period
+  int koff[KPER], voff[4];
+#pragma unroll
+  for (int x = 0; x < KPER; ++x) koff[x] = n * 2 * D + 16 * ((2 * x + g) ^ kswz<D>(n));
+#pragma unroll
+  for (int x = 0; x < 4; ++x) voff[x] = n * 128 + 16 * ((2 * x + g) ^ ((n >> 1) & 7));
+  auto kread = [&](const char* base, int i) {  // S step i: k-block i / 2, key half i % 2
+    const int kb = i >> 1, kh = i & 1;
+    return *reinterpret_cast<const half8*>(base + koff[kb % KPER] + kh * 64 * D + (kb / KPER) * 32 * KPER);
+  };
+  auto vread = [&](const char* base, int i) {  // PV step i: key block i / NDT, d tile i % NDT
+    return *reinterpret_cast<const half8*>(base + voff[i / NDT] + (i % NDT) * 32 * 128);
+  };
+
+  // one pipeline step: MFMA step s of the tile (s < NS1: scores, else PV)
+  constexpr int NS1 = 2 * NKB, NS2 = 4 * NDT;
+  auto frag = [&](const char* kbase, const char* vbase, int st) {
+    return st < NS1 ? kread(kbase, st) : vread(vbase, st - NS1);
+  };
+
+  float16_t O[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) O[t][e] = 0.0f;
+  float l_run = 0.0f;
+
+  const float c2 = p.scale * 1.4426950408889634f;  // scores to log2 units
+  const int key_end = min(kn, offset + q0 + BQ);
+  const int ntiles = (key_end + BK - 1) / BK;
+  // this lane's query sees keys <= lim; accumulator (kh, e) of lane group g
+  // is key j0 + 32 kh + 16 (e / 8) + 8 g + e % 8 of the tile at j0
+  const int lim = min(offset + q0 + 32 * wave + n, kn1);
+  auto key_in_tile = [](int x) { return 32 * (x >> 4) + 16 * ((x >> 3) & 1) + (x & 7); };  // x = 16 kh + e
+
+  // ---- prologue: K(0), K(1), V(0) resident; scores of tile 0
+  issue_k(0, 0);
+  if (ntiles > 1) issue_k(1, BK);
+  issue_v(0, 0);
+  vm_wait_all();
+  lds_barrier();
+  float16_t Sc[2], Sn[2];
+  half8 fb[PD];
+  {
+    const char* kbase = reinterpret_cast<const char*>(sK[0]);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Sc[kh][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PD; ++i) fb[i] = kread(kbase, i);
+#pragma unroll
+    for (int i = 0; i < NS1; ++i) {
+      Sc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[i % PD], qf[i >> 1], Sc[i & 1], 0, 0, 0);
+      if (i + PD < NS1) fb[i % PD] = kread(kbase, i + PD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float m_ref;
+  {
+    const int thr = lim - 8 * g;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+      const float sv = key_in_tile(x) > thr ? -INFINITY : Sc[x >> 4][x & 15];
+      Sc[x >> 4][x & 15] = sv;
+      mx = fmaxf(mx, sv);
+    }
+    m_ref = halves_max(mx);  // finite: every query sees key 0
+  }
+  lds_barrier();  // all waves are done with K(0) before K(2) replaces it
+
+  // ---- software pipeline over key tiles.  Iteration j, with K(j+1) and V(j)
+  // resident and the masked scores of tile j in Sc:
+  //   phase 1: MFMA  Sn = K(j+1) Q^T            VALU  P = exp2(Sc c - m c), row sum
+  //   phase 2: MFMA  O^T += V(j)^T P^T          VALU  mask Sn, row max of tile j+1
+  // then the reference maximum moves (rare) before tile j+1's exponentials.
+  // The DMA of K(j+2) and V(j+1) runs under both phases.  In the last
+  // iteration Sn is computed from a stale buffer and discarded.
+  for (int j = 0; j < ntiles; ++j) {
+    const int j0 = j * BK;
+    if (j + 2 < ntiles) issue_k(j & 1, j0 + 2 * BK);
+    if (j + 1 < ntiles) issue_v((j + 1) & 1, j0 + BK);
+    if (j0 + BK > kn) {  // last tile runs past the keys: zero those value columns
+      half_t* v = sV[j & 1];
+      for (int x = tid; x < D * 8; x += 256) {
+        const int r = x >> 3, slot = x & 7;
+        const int k0 = j0 + 8 * (slot ^ ((r >> 1) & 7));
+        if (k0 + 8 > kn) {
+          half8 val = *reinterpret_cast<half8*>(v + r * 64 + slot * 8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k0 + e >= kn) val[e] = half_t(0);
+          *reinterpret_cast<half8*>(v + r * 64 + slot * 8) = val;
+        }
+      }
+      lds_barrier();
+    }
+    const char* kbase = reinterpret_cast<const char*>(sK[(j + 1) & 1]);
+    const char* vbase = reinterpret_cast<const char*>(sV[j & 1]);
+    const float mc = m_ref * c2;
+    const int thr = lim - (j0 + BK) - 8 * g;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Sn[kh][e] = 0.0f;
+    half8 pf[4];
+    float ps = 0.0f, mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PD; ++i) fb[i] = frag(kbase, vbase, i);
+    // phase 1: EPS1 probabilities per score MFMA
+    constexpr int EPS1 = 32 / NS1, EPS2 = 32 / NS2;
+#pragma unroll
+    for (int st = 0; st < NS1; ++st) {
+      Sn[st & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[st % PD], qf[st >> 1], Sn[st & 1], 0, 0, 0);
+      fb[st % PD] = frag(kbase, vbase, st + PD);
+#pragma unroll
+      for (int u = 0; u < EPS1; ++u) {
+        const int x = st * EPS1 + u;
+        const float pv = __builtin_amdgcn_exp2f(fmaf(Sc[x >> 4][x & 15], c2, -mc));
+        ps += pv;
+        pf[x >> 3][x & 7] = static_cast<half_t>(pv);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // phase 2: EPS2 masked scores of tile j+1 per PV MFMA, two MFMAs behind
+    // the end of the score chain (the last 2 EPS2 follow the loop)
+    auto mask_max = [&](int x) {
+      const float sv = key_in_tile(x) > thr ? -INFINITY : Sn[x >> 4][x & 15];
+      Sc[x >> 4][x & 15] = sv;  // phase 1 is done with tile j's scores
+      mx = fmaxf(mx, sv);
+    };
+#pragma unroll
+    for (int i = 0; i < NS2; ++i) {
+      O[i % NDT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[(NS1 + i) % PD], pf[i / NDT], O[i % NDT], 0, 0, 0);
+      if (NS1 + i + PD < NS1 + NS2) fb[(NS1 + i) % PD] = frag(kbase, vbase, NS1 + i + PD);
+      if (i >= 2) {
+#pragma unroll
+        for (int u = 0; u < EPS2; ++u) mask_max((i - 2) * EPS2 + u);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int x = 32 - 2 * EPS2; x < 32; ++x) mask_max(x);
+    l_run += ps;
+    if (j + 1 < ntiles) {
+      // lazy rescale: move the reference only when exp2 would exceed 2^8
+      const float m_new = fmaxf(m_ref, halves_max(mx));
+      if (__builtin_amdgcn_ballot_w64((m_new - m_ref) * c2 > 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f((m_ref - m_new) * c2);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) O[t][e] *= alpha;
+        l_run *= alpha;
+        m_ref = m_new;
+      }
+    }
+    vm_wait_all();
+    lds_barrier();
+  }
+
+  // ---- epilogue: y = round(round(O / l) * round(sigmoid(gate))).  O^T
+  // accumulator e of tile t holds d = 32 t + 8 (e / 4) + 4 g + e % 4: four
+  // consecutive features per (t, e / 4).  With 8-byte aligned gate and y
+  // rows every gate read is issued before the first store (the loads would
+  // otherwise wait one memory latency each).
+  const float inv = 1.0f / halves_sum(l_run);
+  const int row = q0 + 32 * wave + n;
+  const int64_t prow = qb0 + min(row, qn - 1);  // packed row (clamped for the loads)
+  const half_t* gate = static_cast<const half_t*>(p.gate) + prow * p.ldg + (int64_t)h * p.hsg;
+  half_t* y = static_cast<half_t*>(p.y) + prow * p.ldy + (int64_t)h * d;
+  auto out4 = [&](int t, int blk, half4 gv) {
+    half4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = static_cast<float>(static_cast<half_t>(O[t][4 * blk + e] * inv));
+      const float sg = static_cast<float>(static_cast<half_t>(sigmoid(static_cast<float>(gv[e]))));
+      r[e] = static_cast<half_t>(a * sg);
+    }
+    return r;
+  };
+  if (p.vec_io) {
+    half4 gv[NDT][4];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const int d0 = 32 * t + 8 * blk + 4 * g;
+        gv[t][blk] = d0 < d ? *reinterpret_cast<const half4*>(gate + d0) : half4{};
+      }
+    if (row < qn) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+          const int d0 = 32 * t + 8 * blk + 4 * g;
+          if (d0 < d) *reinterpret_cast<half4*>(y + d0) = out4(t, blk, gv[t][blk]);
+        }
+    }
+  } else if (row < qn) {
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const int d0 = 32 * t + 8 * blk + 4 * g;
+        if (d0 < d) {
+          half4 gv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gv[e] = gate[d0 + e];
+          const half4 r = out4(t, blk, gv);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[d0 + e] = r[e];
+        }
+      }
+  }
+  }  // work items (the last key tile ended with a barrier: LDS is free)
+}
+
+// Query tiles of a ragged batch (one work-group): per sequence its tiles of
+// 128 queries, ranked by key count (most first, ties in sequence order) for
+// a longest-first launch.  Offsets are clamped to [0, T].  Beyond 8192 tiles
+// the ranking is skipped (sequence order).
+__global__ __launch_bounds__(256) void attn_tables(const int* __restrict__ cu, int nseq, int T, int np,
+                                                   int2* __restrict__ pairs, int* __restrict__ npairs,
+                                                   int* __restrict__ keys) {
+  __shared__ int s_total;
+  const int tid = threadIdx.x;
+  const int per = (nseq + 255) / 256;  // consecutive sequences per thread
+  const int s0 = min(tid * per, nseq), s1 = min(s0 + per, nseq);
+  auto length = [&](int s) {
+    const int a = min(max(cu[s], 0), T);
+    return min(max(cu[s + 1], a), T) - a;
+  };
+  auto tiles = [&](int s) { return (length(s) + 127) / 128; };
+  int first = 0;
+  for (int s = 0; s < s0; ++s) first += tiles(s);
+  if (tid == 0) {
+    int t = 0;
+    for (int s = 0; s < nseq; ++s) t += tiles(s);
+    s_total = t;
+    *npairs = t;
+  }
+  int f = first;
+  for (int s = s0; s < s1; ++s) {  // key count of each tile: prefix + its last query's causal reach
+    const int len = length(s), nt = tiles(s);
+    for (int t = 0; t < nt; ++t) keys[f + t] = np + min(128 * (t + 1), len);
+    f += nt;
+  }
+  __threadfence_block();
+  __syncthreads();
+  const int total = s_total;
+  f = first;
+  for (int s = s0; s < s1; ++s) {
+    const int nt = tiles(s);
+    for (int t = 0; t < nt; ++t) {
+      const int i = f + t;
+      int rank = i;
+      if (total <= 8192) {
+        rank = 0;
+        const int ki = keys[i];
+        for (int j = 0; j < total; ++j) rank += (keys[j] > ki) || (keys[j] == ki && j < i);
+      }
+      pairs[rank] = make_int2(s, t);
+    }
+    f += nt;
+  }
+}
+
+// work-groups resident at once (CUs x occupancy of the instance), per device
+template <int D>
+int resident_groups() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16<D>, 256, 0) != hipSuccess || per <= 0) per = 1;
+    cached[dev] = cus * per;
+  }
+  return cached[dev];
+}
+
+template <int D>
+int launch(const AttnParams& p0, hipStream_t s) {
+  AttnParams p = p0;
+  // 8-byte gate and output accesses: every row and head offset a multiple of 4 halves
+  p.vec_io = ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.y)) & 7) == 0 &&
+             p.ldg % 4 == 0 && p.hsg % 4 == 0 && p.ldy % 4 == 0 && p.d % 4 == 0;
+  const int qtiles = p.cu_q ? (p.qn + 127) / 128 + p.nseq : (p.qn + 127) / 128;
+  const int items = qtiles * p.heads;
+  const int groups = items < resident_groups<D>() ? items : resident_groups<D>();
+  hipLaunchKernelGGL((attn_f16<D>), dim3(groups), dim3(256), 0, s, p);
+  return check_launch("attention");
+}
+
+}  // namespace
+
+size_t attn_tables_bytes(int T, int nseq) {
+  const size_t tiles = (size_t)(T + 127) / 128 + nseq;
+  return ((tiles * sizeof(int2) + 255) & ~(size_t)255) + ((tiles * sizeof(int) + 255) & ~(size_t)255) + 256;
+}
+
+void attn_carve_tables(AttnParams& p, void* ws) {
+  const size_t tiles = (size_t)(p.qn + 127) / 128 + p.nseq;
+  char* b = static_cast<char*>(ws);
+  p.pairs = reinterpret_cast<int2*>(b);
+  b += (tiles * sizeof(int2) + 255) & ~(size_t)255;
+  p.npairs = reinterpret_cast<int*>(b + ((tiles * sizeof(int) + 255) & ~(size_t)255));
+}
+
+int attn_f16_tables(const AttnParams& p, hipStream_t s) {
+  const size_t tiles = (size_t)(p.qn + 127) / 128 + p.nseq;
+  int* keys = reinterpret_cast<int*>(reinterpret_cast<char*>(p.pairs) + ((tiles * sizeof(int2) + 255) & ~(size_t)255));
+  hipLaunchKernelGGL(attn_tables, dim3(1), dim3(256), 0, s, p.cu_q, p.nseq, p.qn, p.np, p.pairs, p.npairs, keys);
+  return check_launch("attention tables");
+}
+
+bool attn_f16_ok(const AttnParams& p) {
+  // per-head byte offsets are 32-bit
+  return p.d % 8 == 0 && p.d <= 256 && p.ldv % 8 == 0 && p.ldv >= 64 &&
+         (int64_t)p.ldk * p.d < (int64_t(1) << 30) && (int64_t)p.d * p.ldv < (int64_t(1) << 30);
+}
+
+int attn_f16_launch(const AttnParams& p, hipStream_t s) {
+  if (p.d <= 64) return launch<64>(p, s);
+  if (p.d <= 128) return launch<128>(p, s);
+  return launch<256>(p, s);
+}
+
+}  // namespace clef

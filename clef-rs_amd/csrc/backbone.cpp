@@ -111,17 +111,30 @@ struct Workspace {
   void* scan_ws;
   size_t scan_ws_bytes;
   int ldv;
+  // ragged batches
+  int32_t* cu;      // [nseq + 1] token offsets
+  void* attn_ws;    // attention tables (mixed profile)
+  size_t attn_ws_bytes;
+  void* kseq;       // f32 profile: one sequence's [prefix; own] keys [kvh, prefix + T, d]
+  void* vseq;       // and values [kvh, d, ldvs]
+  int ldvs;
 };
 
 size_t elt(int dtype) { return dtype == CLEF_F32 ? 4 : 2; }
 
-size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base) {
+// nseq > 0: a ragged batch of nseq sequences, T tokens in all, each after the
+// same `prefix` cached tokens (which stay in the prefix state: kh / vt hold
+// the packed new tokens only).
+size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base, int nseq = 0) {
   const clef_backbone_config& c = b->c;
   const size_t a = elt(b->ad);
-  const int Ttot = prefix + T;
+  const int Ttot = (nseq > 0 ? 0 : prefix) + T;
   const int ldv = static_cast<int>(((Ttot + 63) / 64) * 64);
-  const size_t scan_ws = clef_delta_scan_workspace(T, c.lin_k_heads, c.lin_v_heads, c.lin_dk, c.lin_dv, 64,
-                                                   c.scan_precision);
+  const size_t scan_ws =
+      nseq > 0 ? clef_delta_scan_varlen_workspace(T, nseq, c.lin_k_heads, c.lin_v_heads, c.lin_dk, c.lin_dv, 64,
+                                                  c.scan_precision)
+               : clef_delta_scan_workspace(T, c.lin_k_heads, c.lin_v_heads, c.lin_dk, c.lin_dv, 64,
+                                           c.scan_precision);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     char* p = base ? base + off : nullptr;
@@ -147,6 +160,16 @@ size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base
   W.scan_ws = take(scan_ws);
   W.scan_ws_bytes = scan_ws;
   W.ldv = ldv;
+  if (nseq > 0) {
+    W.cu = static_cast<int32_t*>(take(sizeof(int32_t) * (nseq + 1)));
+    W.attn_ws_bytes = clef_attention_varlen_workspace(T, nseq);
+    W.attn_ws = take(W.attn_ws_bytes);
+    if (b->ad == CLEF_F32) {
+      W.ldvs = static_cast<int>(((prefix + T + 63) / 64) * 64);
+      W.kseq = take(a * (size_t)c.kv_heads * (prefix + T) * c.head_dim);
+      W.vseq = take(a * (size_t)c.kv_heads * c.head_dim * W.ldvs);
+    }
+  }
   return off;
 }
 
@@ -518,5 +541,155 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
 #undef TIMED
   if (initial) CLEF_TRY(copy_rows(hidden, init.hidden, 4ull * offset * H, s));
   if (capture) CLEF_TRY(copy_rows(sav.hidden, h, 4ull * capture * H, s));
+  return 0;
+}
+
+extern "C" size_t clef_backbone_varlen_workspace(const clef_backbone* b, int T, int nseq, int prefix_tokens) {
+  if (!b || T < 1 || nseq < 1 || nseq > 4096 || prefix_tokens < 0) return 0;
+  return carve(b, T, prefix_tokens, nullptr, nullptr, nseq) + 256;
+}
+
+// Ragged batch of requests that share one cached prefix (a prefix-cache hit
+// for every request, prefix_cache.rs:135-177): each sequence's hidden states
+// equal clef_backbone_prefill of its ids resumed from `initial`.
+extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids, const int32_t* cu_seqlens,
+                                            int nseq, const void* initial, int initial_tokens, float* hidden,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  CLEF_REQUIRE(b && ids && cu_seqlens && hidden && workspace, "prefill: null argument");
+  CLEF_REQUIRE(nseq >= 1 && nseq <= 4096 && cu_seqlens[0] == 0, "prefill: 1..4096 sequences from offset 0");
+  const clef_backbone_config& c = b->c;
+  const int offset = initial ? initial_tokens : 0;
+  CLEF_REQUIRE(offset >= 0 && (!initial || offset >= 1), "prefill boundary or vocabulary");
+  for (int s = 0; s < nseq; ++s)
+    CLEF_REQUIRE(cu_seqlens[s + 1] > cu_seqlens[s] && (int64_t)offset + cu_seqlens[s + 1] - cu_seqlens[s] <= c.max_tokens,
+                 "prefill: every sequence needs 1..max_tokens - prefix tokens");
+  const int T = cu_seqlens[nseq];
+  CLEF_REQUIRE(T <= (1 << 20), "prefill: at most 2^20 tokens per batch");
+  for (int t = 0; t < T; ++t) CLEF_REQUIRE(ids[t] >= 0 && ids[t] < c.vocab, "prefill boundary or vocabulary");
+  const size_t need = carve(b, T, offset, nullptr, nullptr, nseq);
+  char* base = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(workspace) + 255) & ~static_cast<uintptr_t>(255));
+  CLEF_REQUIRE(workspace_bytes >= need + static_cast<size_t>(base - static_cast<char*>(workspace)),
+               "prefill: workspace too small");
+  Workspace w;
+  carve(b, T, offset, &w, base, nseq);
+  PrefixView init;
+  if (initial) prefix_layout(b, offset, static_cast<char*>(const_cast<void*>(initial)), &init);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int H = c.hidden, ad = b->ad;
+  const size_t a = elt(ad);
+  float* h = hidden;
+  HIP_TRY(hipMemcpyAsync(w.ids, ids, sizeof(int32_t) * T, hipMemcpyHostToDevice, s), "ids upload");
+  HIP_TRY(hipMemcpyAsync(w.cu, cu_seqlens, sizeof(int32_t) * (nseq + 1), hipMemcpyHostToDevice, s),
+          "cu_seqlens upload");
+#define TIMED(cat, flops, bytes, expr) \
+  CLEF_TRY(timed(b, cat, static_cast<double>(flops), static_cast<double>(bytes), s, [&]() { return (expr); }))
+  const double da = static_cast<double>(a);
+  auto gemm_bytes = [&](double M, double N, double K, bool residual) {
+    return da * (M * K + N * K) + (residual ? 8.0 * M * N : da * M * N);
+  };
+  TIMED(CLEF_CAT_OTHER, 0, (4.0 + da) * T * H, clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
+  const int Hv = c.lin_v_heads, dv = c.lin_dv, taps = c.conv_taps;
+  const int heads = c.heads, kvh = c.kv_heads, d = c.head_dim;
+  const double rms_bytes = (4.0 + da) * T * H;
+  // attention pairs: each query sees the prefix and its own earlier tokens
+  double pairs = 0.0;
+  for (int q = 0; q < nseq; ++q) {
+    const double L = cu_seqlens[q + 1] - cu_seqlens[q];
+    pairs += L * offset + 0.5 * L * (L + 1.0);
+  }
+
+  for (int li = 0; li < c.n_layers; ++li) {
+    const LayerState& L = b->layers[li];
+    TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
+    if (L.kind == 0) {
+      const int NP = b->NP, Wc = b->W;
+      char* proj = static_cast<char*>(w.proj);
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * NP * H, gemm_bytes(T, NP, H, false),
+            clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NP, H, ad, ad, CLEF_EPI_STORE, s));
+      const int hist_rows = initial ? (offset < taps - 1 ? offset : taps - 1) : 0;
+      const double ce = static_cast<double>(elt(b->conv_dt));
+      TIMED(CLEF_CAT_CONV, 2.0 * T * Wc * taps, (da + ce) * T * Wc,
+            clef_conv_silu_varlen(proj, NP, ad, initial ? init.hist[li] : nullptr, hist_rows, 0, w.cu, nseq,
+                                  L.conv, taps, w.mixed, Wc, b->conv_dt, T, Wc, s));
+      TIMED(CLEF_CAT_OTHER, 0, (2.0 * da + 8.0) * T * Hv,
+            clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt, L.a_log,
+                             w.g, w.beta, T, Hv, s));
+      const char* mixed = static_cast<const char*>(w.mixed);
+      const size_t ces = elt(b->conv_dt);
+      const double state = 4.0 * Hv * c.lin_dk * dv;
+      const double scan_bytes = ce * T * (2.0 * b->key + b->value) + 8.0 * T * Hv + 4.0 * T * b->value +
+                                (initial ? state : 0.0);
+      TIMED(CLEF_CAT_SCAN, 0, scan_bytes,
+            clef_delta_scan_varlen(mixed, mixed + ces * b->key, mixed + ces * 2 * b->key, Wc, Wc, b->conv_dt, w.g,
+                                   w.beta, Hv, CLEF_F32, w.cu, nseq, T, c.lin_k_heads, Hv, c.lin_dk, dv, 64,
+                                   c.scan_precision, initial ? init.rec[li] : nullptr, 0, w.scan_out,
+                                   (int64_t)Hv * dv, CLEF_F32, nullptr, w.scan_ws, w.scan_ws_bytes, s));
+      TIMED(CLEF_CAT_NORM, 6.0 * T * b->value, (4.0 + 2.0 * da) * T * b->value,
+            clef_gated_rms_silu(w.scan_out, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * H * b->value, gemm_bytes(T, H, b->value, true),
+            clef_gemm(w.gated, b->value, L.out, b->value, h, H, T, H, b->value, ad, ad, CLEF_EPI_RESIDUAL, s));
+    } else {
+      const int NA = b->NA;
+      char* proj = static_cast<char*>(w.proj);
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * NA * H, gemm_bytes(T, NA, H, false),
+            clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
+      const size_t koff = a * 2 * heads * d, voff = koff + a * kvh * d;
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
+            clef_qk_norm_rotary_varlen(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
+                                       c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
+            clef_qk_norm_rotary_varlen(proj + koff, NA, d, ad, L.k_norm, w.kh, T, ad, T, kvh, d, c.rotary_dim,
+                                       c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
+      TIMED(CLEF_CAT_OTHER, 0, 2.0 * da * T * kvh * d,
+            clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, 0, s));
+      if (ad == CLEF_F16) {
+        TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pairs, da * (3.0 * T * heads * d + 2.0 * (T + offset) * kvh * d),
+              clef_attention_gated_varlen(w.qh, T, w.kh, T, w.vt, w.ldv, w.cu, nseq, T,
+                                          initial ? init.key[li] : nullptr, offset,
+                                          initial ? init.val[li] : nullptr, offset, offset, ad, heads, kvh, d,
+                                          proj + a * d, NA, 2 * d, w.gated, (int64_t)heads * d, w.attn_ws,
+                                          w.attn_ws_bytes, s));
+      } else {
+        // f32 profile: one launch per sequence over [prefix; own] keys
+        for (int q = 0; q < nseq; ++q) {
+          const int t0 = cu_seqlens[q], Lq = cu_seqlens[q + 1] - t0, kn = offset + Lq;
+          for (int gk = 0; gk < kvh; ++gk) {
+            char* kd = static_cast<char*>(w.kseq) + a * (size_t)gk * kn * d;
+            if (initial)
+              CLEF_TRY(copy_rows(kd, static_cast<char*>(init.key[li]) + a * (size_t)gk * offset * d,
+                                 a * (size_t)offset * d, s));
+            CLEF_TRY(copy_rows(kd + a * (size_t)offset * d,
+                               static_cast<char*>(w.kh) + a * ((size_t)gk * T + t0) * d, a * (size_t)Lq * d, s));
+          }
+          if (initial)
+            HIP_TRY(hipMemcpy2DAsync(w.vseq, a * w.ldvs, init.val[li], a * offset, a * offset, (size_t)kvh * d,
+                                     hipMemcpyDeviceToDevice, s),
+                    "value prefix copy");
+          HIP_TRY(hipMemcpy2DAsync(static_cast<char*>(w.vseq) + a * offset, a * w.ldvs,
+                                   static_cast<char*>(w.vt) + a * t0, a * w.ldv, a * Lq, (size_t)kvh * d,
+                                   hipMemcpyDeviceToDevice, s),
+                  "value copy");
+          const double pq = static_cast<double>(Lq) * offset + 0.5 * Lq * (Lq + 1.0);
+          TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pq, da * (3.0 * Lq * heads * d + 2.0 * kn * kvh * d),
+                clef_attention_gated(static_cast<char*>(w.qh) + a * (size_t)t0 * d, T, w.kseq, kn, w.vseq, w.ldvs,
+                                     ad, heads, kvh, Lq, kn, d, proj + a * ((size_t)t0 * NA + d), NA, 2 * d,
+                                     static_cast<char*>(w.gated) + a * (size_t)t0 * heads * d, (int64_t)heads * d,
+                                     s));
+        }
+      }
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * H * heads * d, gemm_bytes(T, H, heads * d, true),
+            clef_gemm(w.gated, heads * d, L.out, heads * d, h, H, T, H, heads * d, ad, ad, CLEF_EPI_RESIDUAL, s));
+    }
+    TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.post_norm, w.n, H, ad, T, H, c.eps, s));
+    const double I = c.intermediate;
+    TIMED(CLEF_CAT_GEMM, 4.0 * T * I * H, da * (T * H + 2.0 * I * H + T * I),
+          clef_gemm_swiglu(w.n, H, L.gate, L.up, H, w.mlp, c.intermediate, T, c.intermediate, H, ad, s));
+    TIMED(CLEF_CAT_GEMM, 2.0 * T * I * H, gemm_bytes(T, H, I, true),
+          clef_gemm(w.mlp, c.intermediate, L.down, c.intermediate, h, H, T, H, c.intermediate, ad, ad,
+                    CLEF_EPI_RESIDUAL, s));
+  }
+  TIMED(CLEF_CAT_NORM, 4.0 * T * H, 8.0 * T * H, clef_rms_norm(h, H, CLEF_F32, b->final_norm, h, H, CLEF_F32, T, H, c.eps, s));
+#undef TIMED
   return 0;
 }

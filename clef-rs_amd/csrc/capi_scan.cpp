@@ -54,13 +54,11 @@ extern "C" size_t clef_delta_scan_workspace(int T, int Hk, int Hv, int dk, int d
   return clef::scan_workspace_bytes(T, Hk, Hv, dk, precision);
 }
 
-extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk,
-                               int64_t sv, int dtype_qkv, const void* g, const void* beta,
-                               int64_t sgb, int dtype_gb, int T, int Hk, int Hv, int dk, int dv,
-                               int chunk, int precision, const float* initial, int capture,
-                               void* out, int64_t so, int dtype_out, float* captured,
-                               float* final_state, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+// shared validation and parameter set-up of both scan entry points
+static int scan_params(clef::ScanParams& p, const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
+                       int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb, int T, int Hk,
+                       int Hv, int dk, int dv, int chunk, int precision, void* out, int64_t so, int dtype_out,
+                       void* workspace, size_t workspace_bytes, int nseq) {
   if (int rc = scan_dims(T, Hk, Hv, dk, dv, chunk, precision)) return rc;
   CLEF_REQUIRE(q && k && v && g && beta && out, "DeltaNet scan: null input or output");
   CLEF_REQUIRE(valid_dtype(dtype_qkv) && valid_dtype(dtype_gb) && valid_dtype(dtype_out),
@@ -75,25 +73,66 @@ extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int6
   // a chunk's rows of v and out are addressed with 32-bit byte offsets
   CLEF_REQUIRE(sv < (int64_t(1) << 22) && so < (int64_t(1) << 22),
                "DeltaNet scan: token stride of v or out above 2^22 elements");
-  CLEF_REQUIRE(capture >= 0 && capture <= T, "DeltaNet scan: capture must be in 0..T");
-  CLEF_REQUIRE(capture == 0 || captured, "DeltaNet scan: capture requested without a buffer");
-  const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, dk, precision);
+  const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, dk, precision, nseq);
   CLEF_REQUIRE(workspace && workspace_bytes >= need, "DeltaNet scan: workspace too small");
   CLEF_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
                "DeltaNet scan: workspace must be 256-byte aligned");
-
-  clef::ScanParams p{};
+  p = clef::ScanParams{};
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta;
   p.sqk = sqk; p.sv = sv; p.sgb = sgb; p.so = so;
   p.dtype_qkv = dtype_qkv; p.dtype_gb = dtype_gb; p.dtype_out = dtype_out;
   p.T = T; p.Hk = Hk; p.Hv = Hv; p.dk = dk; p.dv = dv;
-  p.nchunks = (T + 63) / 64;
+  p.nchunks = (T + 63) / 64 + nseq;  // ragged: the most chunks nseq sequences of T tokens can have
   const int vi = dtype_qkv == CLEF_F32 ? 4 : 8;
   p.vec_qk = (dk % vi == 0) && (sqk % vi == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0) &&
              ((reinterpret_cast<uintptr_t>(k) & 15) == 0);
   p.qscale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dk)));
+  p.out = out;
+  p.nseq = nseq;
+  return 0;
+}
+
+extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk,
+                               int64_t sv, int dtype_qkv, const void* g, const void* beta,
+                               int64_t sgb, int dtype_gb, int T, int Hk, int Hv, int dk, int dv,
+                               int chunk, int precision, const float* initial, int capture,
+                               void* out, int64_t so, int dtype_out, float* captured,
+                               float* final_state, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  clef::ScanParams p;
+  if (int rc = scan_params(p, q, k, v, sqk, sv, dtype_qkv, g, beta, sgb, dtype_gb, T, Hk, Hv, dk, dv, chunk,
+                           precision, out, so, dtype_out, workspace, workspace_bytes, 0))
+    return rc;
+  CLEF_REQUIRE(capture >= 0 && capture <= T, "DeltaNet scan: capture must be in 0..T");
+  CLEF_REQUIRE(capture == 0 || captured, "DeltaNet scan: capture requested without a buffer");
   p.initial = initial; p.capture = capture;
-  p.out = out; p.captured = captured; p.final_state = final_state;
+  p.captured = captured; p.final_state = final_state;
+  clef::scan_carve_workspace(p, workspace, precision);
+  return clef::scan_launch(p, precision, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t clef_delta_scan_varlen_workspace(int T, int nseq, int Hk, int Hv, int dk, int dv, int chunk,
+                                                   int precision) {
+  if (scan_dims(T, Hk, Hv, dk, dv, chunk, precision) || nseq < 1 || nseq > 4096) return 0;
+  return clef::scan_workspace_bytes(T, Hk, Hv, dk, precision, nseq);
+}
+
+extern "C" int clef_delta_scan_varlen(const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
+                                      int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
+                                      const int32_t* cu_seqlens, int nseq, int T, int Hk, int Hv, int dk, int dv,
+                                      int chunk, int precision, const float* initial, int64_t initial_stride,
+                                      void* out, int64_t so, int dtype_out, float* final_states, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  CLEF_REQUIRE(cu_seqlens && nseq >= 1 && nseq <= 4096, "DeltaNet scan: cu_seqlens and 1 <= nseq <= 4096");
+  CLEF_REQUIRE(initial_stride >= 0, "DeltaNet scan: negative initial-state stride");
+  clef::ScanParams p;
+  if (int rc = scan_params(p, q, k, v, sqk, sv, dtype_qkv, g, beta, sgb, dtype_gb, T, Hk, Hv, dk, dv, chunk,
+                           precision, out, so, dtype_out, workspace, workspace_bytes, nseq))
+    return rc;
+  p.initial = initial;
+  p.init_stride = initial_stride;
+  p.final_state = final_states;
+  p.cu_seqlens = cu_seqlens;
   clef::scan_carve_workspace(p, workspace, precision);
   return clef::scan_launch(p, precision, static_cast<hipStream_t>(stream));
 }

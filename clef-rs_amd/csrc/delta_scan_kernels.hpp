@@ -186,6 +186,35 @@ __device__ __forceinline__ void dma_block(const void* src_lane, void* lds_block)
 }
 
 // ---------------------------------------------------------------------------
+// Token span of chunk c (ragged batches: from the chunk table; false past
+// its last chunk).
+__device__ __forceinline__ bool chunk_span(const ScanParams& p, int c, int& t0, int& n) {
+  if (p.chunk_tab) {
+    if (c >= *p.nchunk_total) return false;
+    const int2 e = p.chunk_tab[c];
+    t0 = e.x;
+    n = e.y;
+  } else {
+    t0 = c * kC;
+    n = min(kC, p.T - t0);
+  }
+  return true;
+}
+
+// Token span of chunk c in the carry, with the batch kind known at compile
+// time (one sequence: no table lookups on the recurrence's path).
+template <bool VL>
+__device__ __forceinline__ void chunk_at(const ScanParams& p, int c, int& t0, int& n) {
+  if constexpr (VL) {
+    const int2 e = p.chunk_tab[c];
+    t0 = e.x;
+    n = e.y;
+  } else {
+    t0 = c * kC;
+    n = min(kC, p.T - t0);
+  }
+}
+
 // Kernel 1: per (chunk, k-head) preparation of every state-independent
 // operand of the chunk, for all v-heads of the k-head.
 // ---------------------------------------------------------------------------
@@ -223,8 +252,8 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   const int rep = p.Hv / p.Hk;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int col = lane & 15, grp = lane >> 4;
-  const int t0 = chunk * kC;
-  const int n = min(kC, p.T - t0);
+  int t0, n;
+  if (!chunk_span(p, chunk, t0, n)) return;  // grid sized for the most chunks a batch can have
   const int dk = p.dk;
   const int64_t ck = (int64_t)chunk * p.Hk + hk;
   const int cap_chunk = p.capture > 0 ? (p.capture - 1) / kC : -1;
@@ -496,19 +525,23 @@ struct CarryCtx {
   bool col_ok;
   int lane, col, grp;
   int nchunks, cap_chunk, cap_row;
+  int c0;             // the sequence's first chunk
+  const float* init;  // the sequence's initial state [Hv][dk][dv] or null
+  float* fin;         // its final state or null
 };
 
 // wave 1: K^, U and scalars of chunk i+D0-1 into the ring during chunk i.
-template <class CT, int DK>
+template <class CT, int DK, bool VL>
 __device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x,
                                              typename Carry<CT, DK>::frag* ring) {
   typedef Carry<CT, DK> K;
   typedef typename K::G G;
   auto issue = [&](int c) {
     typename K::frag* slot = ring + (c % K::D0) * K::SLOT;
-    const char* kf = static_cast<const char*>(p.Kf) + (((int64_t)c * p.Hk + x.hk) * G::NBK * 64 + x.lane) * 16;
-    const char* uf = static_cast<const char*>(p.Uf) + (((int64_t)c * p.Hv + x.h) * G::NBU * 64 + x.lane) * 16;
-    const char* sc = reinterpret_cast<const char*>(p.sc + ((int64_t)c * p.Hv + x.h) * 256) + x.lane * 16;
+    const int64_t cg = (VL ? x.c0 : 0) + c;
+    const char* kf = static_cast<const char*>(p.Kf) + ((cg * p.Hk + x.hk) * G::NBK * 64 + x.lane) * 16;
+    const char* uf = static_cast<const char*>(p.Uf) + ((cg * p.Hv + x.h) * G::NBU * 64 + x.lane) * 16;
+    const char* sc = reinterpret_cast<const char*>(p.sc + (cg * p.Hv + x.h) * 256) + x.lane * 16;
 #pragma unroll
     for (int b = 0; b < G::NBK; ++b) dma_block(kf + b * 1024, slot + b * 64);
 #pragma unroll
@@ -532,7 +565,7 @@ __device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx
 }
 
 // wave 0: the recurrence.  IT = dtype of v.
-template <class CT, int DK, class IT>
+template <class CT, int DK, class IT, bool VL>
 __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const CarryCtx& x,
                                                  const typename Carry<CT, DK>::frag* ring,
                                                  typename Carry<CT, DK>::frag* hand) {
@@ -542,6 +575,8 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
   constexpr int NST = G::NST, NKX = G::NKX, NKT = G::NKT, NBK = G::NBK, NBU = G::NBU, TPK = G::TPK;
   const int lane = x.lane, grp = x.grp;
   const int dk = p.dk, dv = p.dv;
+  const float* init = VL ? x.init : p.initial;
+  float* fin = VL ? x.fin : p.final_state;
 
   float4_t S[NST];
 #pragma unroll
@@ -550,7 +585,7 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
     for (int i = 0; i < 4; ++i) {
       const int row = slot_index<CT>(s, 4 * grp + i);
       float v = 0.0f;
-      if (p.initial && row < dk && x.col_ok) v = p.initial[((int64_t)x.h * dk + row) * dv + x.jc];
+      if (init && row < dk && x.col_ok) v = init[((int64_t)x.h * dk + row) * dv + x.jc];
       S[s][i] = v;
     }
   frag Sf[NKX];
@@ -567,8 +602,8 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
     for (int i = 0; i < 4; ++i)
       voff[4 * t + i] = x.col_ok ? (slot_index<CT>(t, 4 * grp + i) * (int)p.sv + x.col) * (int)sizeof(IT) : kOOB;
   auto load_v = [&](uint32_t* vb, int c) {
-    const int cc = min(c, x.nchunks - 1);
-    const int t0 = cc * kC, n = min(kC, p.T - t0);
+    int t0, n;
+    chunk_at<VL>(p, (VL ? x.c0 : 0) + min(c, x.nchunks - 1), t0, n);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(vbase + (int64_t)t0 * p.sv, n * (int)p.sv * (int)sizeof(IT));
 #pragma unroll
     for (int k = 0; k < 16; ++k) vb[k] = buffer_load_bits<IT>(r, voff[k]);
@@ -679,13 +714,13 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
   if (i < x.nchunks) step(i, va);
   lds_barrier();  // outputs of the last chunk
 
-  if (p.final_state) {
+  if (fin) {
 #pragma unroll
     for (int s = 0; s < NST; ++s)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int row = slot_index<CT>(s, 4 * grp + j);
-        if (row < dk && x.col_ok) p.final_state[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
+        if (row < dk && x.col_ok) fin[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
       }
   }
 }
@@ -693,7 +728,7 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
 // wave 0, f16 operands: the recurrence with the LDS reads of each round
 // interleaved with the MFMAs of the previous one (a wave issues one 1 KiB
 // read per ~14 cycles, an MFMA per 18).  IT = dtype of v.
-template <class CT, int DK, class IT>
+template <class CT, int DK, class IT, bool VL>
 __device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const CarryCtx& x,
                                                      const typename Carry<CT, DK>::frag* ring,
                                                      typename Carry<CT, DK>::frag* hand) {
@@ -704,6 +739,8 @@ __device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const 
   static_assert(G::NKT == 2 && G::TPK == 2, "f16 geometry");
   const int lane = x.lane, grp = x.grp;
   const int dk = p.dk, dv = p.dv;
+  const float* init = VL ? x.init : p.initial;
+  float* fin = VL ? x.fin : p.final_state;
 
   float4_t S[NST];
 #pragma unroll
@@ -712,7 +749,7 @@ __device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const 
     for (int i = 0; i < 4; ++i) {
       const int row = slot_index<CT>(s, 4 * grp + i);
       float v = 0.0f;
-      if (p.initial && row < dk && x.col_ok) v = p.initial[((int64_t)x.h * dk + row) * dv + x.jc];
+      if (init && row < dk && x.col_ok) v = init[((int64_t)x.h * dk + row) * dv + x.jc];
       S[s][i] = v;
     }
   frag Sf[NKX];
@@ -729,8 +766,8 @@ __device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const 
     for (int j = 0; j < 4; ++j)
       voff[4 * q + j] = x.col_ok ? (slot_index<CT>(q, 4 * grp + j) * (int)p.sv + x.col) * (int)sizeof(IT) : kOOB;
   auto load_v = [&](uint32_t* vb, int c) {
-    const int cc = min(c, x.nchunks - 1);
-    const int t0 = cc * kC, n = min(kC, p.T - t0);
+    int t0, n;
+    chunk_at<VL>(p, (VL ? x.c0 : 0) + min(c, x.nchunks - 1), t0, n);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(vbase + (int64_t)t0 * p.sv, n * (int)p.sv * (int)sizeof(IT));
 #pragma unroll
     for (int k = 0; k < 16; ++k) vb[k] = buffer_load_bits<IT>(r, voff[k]);
@@ -833,19 +870,19 @@ __device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const 
   if (i < x.nchunks) step(i, va);
   lds_barrier();  // outputs of the last chunk
 
-  if (p.final_state) {
+  if (fin) {
 #pragma unroll
     for (int s = 0; s < NST; ++s)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int row = slot_index<CT>(s, 4 * grp + j);
-        if (row < dk && x.col_ok) p.final_state[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
+        if (row < dk && x.col_ok) fin[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
       }
   }
 }
 
 // waves 2-3: O of chunk c during chunk c+1, rows 16t.. for t = 2(wave-2)+{0,1}.
-template <class CT, int DK, class OT>
+template <class CT, int DK, class OT, bool VL>
 __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCtx& x, int ow,
                                               const typename Carry<CT, DK>::frag* hand) {
   typedef Carry<CT, DK> K;
@@ -859,10 +896,10 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
     float4_t eg[2];
   };
   auto load_o = [&](Ops& o, int c) {
-    const int cc = min(c, x.nchunks - 1);
-    const frag* qf = static_cast<const frag*>(p.Qf) + ((int64_t)cc * p.Hk + x.hk) * G::NBK * 64 + lane;
-    const frag* nf = static_cast<const frag*>(p.Nf) + ((int64_t)cc * p.Hv + x.h) * G::NBN * 64 + lane;
-    const float* scs = p.sc + ((int64_t)cc * p.Hv + x.h) * 256;
+    const int64_t cc = (VL ? x.c0 : 0) + min(c, x.nchunks - 1);
+    const frag* qf = static_cast<const frag*>(p.Qf) + (cc * p.Hk + x.hk) * G::NBK * 64 + lane;
+    const frag* nf = static_cast<const frag*>(p.Nf) + (cc * p.Hv + x.h) * G::NBN * 64 + lane;
+    const float* scs = p.sc + (cc * p.Hv + x.h) * 256;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int t = 2 * ow + tt;
@@ -892,7 +929,8 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
     for (int kb = 0; kb < NKX; ++kb) sf[kb] = hs[kb * 64 + lane];
 #pragma unroll
     for (int b = 0; b < NKT; ++b) yf[b] = hs[(NKX + b) * 64 + lane];
-    const int t0 = c * kC, n = min(kC, p.T - t0);
+    int t0, n;
+    chunk_at<VL>(p, (VL ? x.c0 : 0) + c, t0, n);
     // rows past the end of the sequence fall outside the buffer range: dropped
     const __amdgpu_buffer_rsrc_t r = make_rsrc(out + (int64_t)t0 * p.so, n * (int)p.so * (int)sizeof(OT));
 #pragma unroll
@@ -917,7 +955,7 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
   if (c < x.nchunks) ostep(c, oa);
 }
 
-template <class CT, int DK>
+template <class CT, int DK, bool VL>
 __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   typedef Carry<CT, DK> K;
   __shared__ __attribute__((aligned(16))) typename K::frag ring[K::D0 * K::SLOT];
@@ -928,41 +966,63 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   x.col = x.lane & 15;
   x.grp = x.lane >> 4;
   const int wave = wave_id();
-  // XCD-aware placement: logical work-group L -> consecutive L share a k-head.
+  // XCD-aware placement for one sequence: logical work-group L -> consecutive
+  // L share a k-head.  A ragged batch keeps the launch order (sequences with
+  // the most chunks first) across all XCDs instead.
   const int nwg = gridDim.x;
   int L = blockIdx.x;
-  if ((nwg & 7) == 0) L = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  if (!VL && (nwg & 7) == 0) L = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
   const int ntiles = (p.dv + kVT - 1) / kVT;
   const int rep = p.Hv / p.Hk;
+  const int slot = L / (p.Hv * ntiles);
+  L -= slot * p.Hv * ntiles;
+  int seq = 0;
+  x.c0 = 0;
+  x.nchunks = p.nchunks;
+  if (VL) {
+    const int4 e = p.seq_tab[slot];
+    seq = e.x;
+    x.c0 = e.y;
+    x.nchunks = e.z;
+  }
   x.h = L / ntiles;
   x.hk = x.h / rep;
   x.j0 = (L % ntiles) * kVT;
   x.jc = x.j0 + x.col;
   x.col_ok = x.jc < p.dv;
   x.jcc = min(x.jc, p.dv - 1);
-  x.nchunks = p.nchunks;
+  x.init = p.initial ? p.initial + seq * p.init_stride : nullptr;
+  x.fin = p.final_state ? p.final_state + (int64_t)seq * p.Hv * p.dk * p.dv : nullptr;
   x.cap_chunk = p.capture > 0 ? (p.capture - 1) / kC : -1;
   x.cap_row = p.capture > 0 ? (p.capture - 1) % kC : 0;
 
+  if (VL && x.nchunks == 0) {  // empty sequence: the final state is the initial one
+    if (wave == 0 && x.fin && x.col_ok)
+      for (int r = x.grp; r < p.dk; r += 4) {
+        const int64_t o = ((int64_t)x.h * p.dk + r) * p.dv + x.jc;
+        x.fin[o] = x.init ? x.init[o] : 0.0f;
+      }
+    return;
+  }
   if (wave == 1) {
-    carry_loader<CT, DK>(p, x, ring);
+    carry_loader<CT, DK, VL>(p, x, ring);
   } else if (wave == 0) {
     if constexpr (sizeof(CT) == 2) {
       if (p.dtype_qkv == 0)
-        carry_recurrence_f16<CT, DK, float>(p, x, ring, hand);
+        carry_recurrence_f16<CT, DK, float, VL>(p, x, ring, hand);
       else
-        carry_recurrence_f16<CT, DK, half_t>(p, x, ring, hand);
+        carry_recurrence_f16<CT, DK, half_t, VL>(p, x, ring, hand);
     } else {
       if (p.dtype_qkv == 0)
-        carry_recurrence<CT, DK, float>(p, x, ring, hand);
+        carry_recurrence<CT, DK, float, VL>(p, x, ring, hand);
       else
-        carry_recurrence<CT, DK, half_t>(p, x, ring, hand);
+        carry_recurrence<CT, DK, half_t, VL>(p, x, ring, hand);
     }
   } else {
     if (p.dtype_out == 0)
-      carry_outputs<CT, DK, float>(p, x, wave - 2, hand);
+      carry_outputs<CT, DK, float, VL>(p, x, wave - 2, hand);
     else
-      carry_outputs<CT, DK, half_t>(p, x, wave - 2, hand);
+      carry_outputs<CT, DK, half_t, VL>(p, x, wave - 2, hand);
   }
 }
 
@@ -972,7 +1032,11 @@ int launch_dk(const ScanParams& p, hipStream_t stream) {
   int rc = check_launch("scan_prepare");
   if (rc) return rc;
   const int ntiles = (p.dv + kVT - 1) / kVT;
-  hipLaunchKernelGGL((scan_carry<CT, DK>), dim3(p.Hv * ntiles), dim3(256), 0, stream, p);
+  const int nseq = p.seq_tab ? p.nseq : 1;
+  if (p.seq_tab)
+    hipLaunchKernelGGL((scan_carry<CT, DK, true>), dim3(nseq * p.Hv * ntiles), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((scan_carry<CT, DK, false>), dim3(p.Hv * ntiles), dim3(256), 0, stream, p);
   return check_launch("scan_carry");
 }
 

@@ -26,10 +26,12 @@ constexpr int kBM = 256, kBK = 64;
 // wait for all DMAs in flight, i.e. for the next stage, before computing on
 // the current one).  Completion is awaited explicitly (vmcnt) before the
 // barrier that publishes a stage.  The LDS destination goes in M0 (low 32
-// bits of the LDS address); lane l writes 16 bytes at M0 + 16 l.
+// bits of the LDS address); lane l writes 16 bytes at M0 + 16 l.  The asm
+// carries the one wait state an LDS DMA needs after the SALU write of M0
+// (the compiler does not see the DMA inside the asm).
 __device__ __forceinline__ void dma16(const void* src_lane, void* lds_block) {
   const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_block));
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src_lane), "{m0}"(m0) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "{m0}"(m0) : "memory");
 }
 
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }

@@ -147,6 +147,135 @@ __global__ __launch_bounds__(256) void conv_silu_vec_kernel(const TI* __restrict
   }
 }
 
+// Sequence of packed token t: the last s with cu[s] <= t (cu has nseq + 1
+// entries; any table gives an index in 0..nseq-1).
+__device__ __forceinline__ int seq_of(const int* __restrict__ cu, int nseq, int t) {
+  int lo = 0, hi = nseq - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Ragged batch of the vectorised conv: tokens cu[s] .. cu[s+1]-1 form sequence
+// s, whose first taps-1 inputs come from its history rows (hist + s * hs, f32
+// [hrows, W]).  A run of kConvRun tokens restarts its window at each sequence
+// start.  Rows are read only in [max(cu[s], 0), t] of the current token t.
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restrict__ x, int64_t ldx,
+                                                               const float* __restrict__ hist, int hrows,
+                                                               int64_t hs, const int* __restrict__ cu, int nseq,
+                                                               const float* __restrict__ w, int taps,
+                                                               TO* __restrict__ y, int64_t ldy, int T, int W) {
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c0 >= W) return;
+  const int t0 = blockIdx.y * kConvRun;
+  float wt[8][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wt[j][k] = k < taps ? w[(int64_t)(c0 + j) * taps + k] : 0.0f;
+  // row tp of sequence s (first token `start`): x row, history row, or zero
+  auto load_row = [&](int s, int start, int tp, float (&v)[8]) {
+    const int hr = hrows + (tp - start);
+    if (tp >= start && tp >= 0) {
+      const TI* src = x + (int64_t)tp * ldx + c0;
+      if (sizeof(TI) == 2) {
+        const half8 h = *reinterpret_cast<const half8*>(src);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(h[j]);
+      } else {
+        const float4_t a = *reinterpret_cast<const float4_t*>(src);
+        const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
+      }
+    } else if (tp < start && hr >= 0 && hist) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = hist[(int64_t)s * hs + (int64_t)hr * W + c0 + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+  };
+  const int t1 = min(t0 + kConvRun, T);
+  int s = seq_of(cu, nseq, t0);
+  int t = t0;
+  while (t < t1) {
+    while (s + 1 < nseq && cu[s + 1] <= t) ++s;
+    const int start = cu[s];
+    const int end = s + 1 < nseq ? min(max(cu[s + 1], t + 1), t1) : t1;
+    float win[4][8];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) load_row(s, start, t - 3 + k, win[k + 1]);
+    for (; t < end; ++t) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) win[k][j] = win[k + 1][j];
+      load_row(s, start, t, win[3]);
+      // a delay reaches before the sequence's history: no term (as the
+      // single-sequence kernel does before row 0)
+      const int avail = hrows + (t - start);
+      TO out[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float acc = 0.0f;  // taps oldest -> newest, each product rounded before the add
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int tap = k - (4 - taps);
+          if (tap >= 0 && avail - (3 - k) >= 0) acc = __fadd_rn(acc, __fmul_rn(win[k][j], wt[j][tap]));
+        }
+        out[j] = static_cast<TO>(acc / (1.0f + expf(-acc)));
+      }
+      TO* dst = y + (int64_t)t * ldy + c0;
+      if (sizeof(TO) == 2) {
+        half8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(out[j]);
+        *reinterpret_cast<half8*>(dst) = h;
+      } else {
+        float4_t a, b;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = static_cast<float>(out[j]), b[j] = static_cast<float>(out[4 + j]);
+        *reinterpret_cast<float4_t*>(dst) = a;
+        *reinterpret_cast<float4_t*>(dst + 4) = b;
+      }
+    }
+  }
+}
+
+// Ragged batch, any layout: one (token, channel) per thread, the same tap
+// order and roundings as conv_silu_kernel over [its sequence's history; its
+// tokens].
+__global__ __launch_bounds__(256) void conv_silu_varlen_scalar(const void* x, int64_t ldx, int dti,
+                                                               const float* hist, int hrows, int64_t hs,
+                                                               const int* __restrict__ cu, int nseq,
+                                                               const float* w, int taps, void* y, int64_t ldy,
+                                                               int dto, int T, int W) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)T * W) return;
+  const int t = static_cast<int>(idx / W), c = static_cast<int>(idx % W);
+  const int s = seq_of(cu, nseq, t);
+  const int start = cu[s];
+  float acc = 0.0f;
+  for (int tap = 0; tap < taps; ++tap) {
+    const int tp = t - (taps - 1 - tap);  // packed row of this delay
+    const int hr = hrows + (tp - start);  // its row in [history; tokens]
+    if (hr < 0) continue;
+    float v;
+    if (tp >= start && tp >= 0)
+      v = ld(x, (int64_t)tp * ldx + c, dti);
+    else if (hist)
+      v = hist[(int64_t)s * hs + (int64_t)hr * W + c];
+    else
+      continue;
+    acc = __fadd_rn(acc, __fmul_rn(v, w[(int64_t)c * taps + tap]));
+  }
+  st(y, (int64_t)t * ldy + c, dto, acc / (1.0f + expf(-acc)));
+}
+
 // Row RMSNorm with the row held in registers: one wave per row, VPL values
 // per lane loaded as 4-wide vectors (width == 4 * 64 * (VPL/4) exactly).
 template <int VPL, class TO>
@@ -277,7 +406,8 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int6
                                                              int64_t ldy_tok, int dto, int T,
                                                              int heads, int d, int rot, int pos0,
                                                              int dst_offset, float eps,
-                                                             float inv_width, RotaryTable tab) {
+                                                             float inv_width, RotaryTable tab,
+                                                             const int* __restrict__ cu, int nseq) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);  // (t, head)
   const int lane = threadIdx.x & 63;
   if (row >= T * heads) return;
@@ -291,7 +421,8 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int6
   s = wave_sum(s);
   const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
   const int half = rot / 2;
-  const float p = static_cast<float>(pos0 + t);
+  // position: pos0 + t, or pos0 + (t - first token of t's sequence)
+  const float p = static_cast<float>(pos0 + (cu ? t - cu[seq_of(cu, nseq, t)] : t));
   const int64_t dst = ((int64_t)h * ldy_tok + dst_offset + t) * d;
   for (int i = lane; i < d; i += 64) {
     const float v = rnd(__fmul_rn(__fmul_rn(ld(x, src + i, dti), inverse), w[i]), dto);
@@ -427,6 +558,44 @@ extern "C" int clef_conv_silu(const void* x, int64_t ldx, int dtype_in, const fl
   return check_launch("conv_silu");
 }
 
+extern "C" int clef_conv_silu_varlen(const void* x, int64_t ldx, int dtype_in, const float* history,
+                                     int history_rows, int64_t history_stride, const int32_t* cu_seqlens,
+                                     int nseq, const float* w, int taps, void* y, int64_t ldy, int dtype_out,
+                                     int T, int W, void* stream) {
+  if (ldx == 0) ldx = W;
+  if (ldy == 0) ldy = W;
+  CLEF_REQUIRE(x && w && y && cu_seqlens && nseq >= 1, "conv: null pointer or no sequences");
+  CLEF_REQUIRE(T >= 1 && W >= 1 && ldx >= W && ldy >= W, "conv: dimensions");
+  CLEF_REQUIRE(taps >= 1 && taps <= 8 && history_rows >= 0 && history_rows <= taps - 1 &&
+                   (history_rows == 0 || history) && history_stride >= 0,
+               "conv: taps or history");
+  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "conv: dtype");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!(taps <= 4 && W % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(y) & 15) == 0)) {
+    const int64_t n = (int64_t)T * W;
+    hipLaunchKernelGGL(conv_silu_varlen_scalar, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, ldx,
+                       dtype_in, history, history_rows, history_stride, cu_seqlens, nseq, w, taps, y, ldy, dtype_out,
+                       T, W);
+    return check_launch("conv_silu_varlen");
+  }
+  const dim3 g((W / 8 + 255) / 256, (T + kConvRun - 1) / kConvRun);
+#define CLEF_CONV_VL(TI, TO)                                                                                   \
+  hipLaunchKernelGGL((conv_silu_varlen_kernel<TI, TO>), g, dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
+                     history, history_rows, history_stride, cu_seqlens, nseq, w, taps, static_cast<TO*>(y), ldy, \
+                     T, W)
+  if (dtype_in == CLEF_F16 && dtype_out == CLEF_F16)
+    CLEF_CONV_VL(half_t, half_t);
+  else if (dtype_in == CLEF_F16)
+    CLEF_CONV_VL(half_t, float);
+  else if (dtype_out == CLEF_F16)
+    CLEF_CONV_VL(float, half_t);
+  else
+    CLEF_CONV_VL(float, float);
+#undef CLEF_CONV_VL
+  return check_launch("conv_silu_varlen");
+}
+
 extern "C" int clef_delta_gates(const void* a, int64_t lda, const void* b, int64_t ldb, int dtype_in,
                                 const float* dt, const float* a_log, float* g, float* beta, int T,
                                 int Hv, void* stream) {
@@ -490,7 +659,30 @@ extern "C" int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int d
   hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
                      rot_dim, pos0, dst_offset, eps, static_cast<float>(1.0 / static_cast<double>(d)),
-                     tab);
+                     tab, nullptr, 0);
+  return check_launch("qk_norm_rotary");
+}
+
+extern "C" int clef_qk_norm_rotary_varlen(const void* x, int64_t ldx, int64_t hs, int dtype_in, const float* w,
+                                          void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
+                                          int rot_dim, double theta, int pos0, const int32_t* cu_seqlens,
+                                          int nseq, int dst_offset, float eps, void* stream) {
+  if (hs == 0) hs = d;
+  if (ldx == 0) ldx = (int64_t)heads * hs;
+  CLEF_REQUIRE(x && w && y && cu_seqlens && nseq >= 1, "q/k norm: null pointer or no sequences");
+  CLEF_REQUIRE(T >= 1 && heads >= 1 && d >= 1 && hs >= d && ldx >= (int64_t)(heads - 1) * hs + d,
+               "q/k norm: dimensions");
+  CLEF_REQUIRE(rot_dim >= 0 && rot_dim <= d && rot_dim % 2 == 0 && rot_dim / 2 <= 128,
+               "q/k norm: rotary width");
+  CLEF_REQUIRE(dst_offset >= 0 && ldy_tok >= (int64_t)dst_offset + T && pos0 >= 0, "q/k norm: destination");
+  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "q/k norm: dtype");
+  RotaryTable tab{};
+  for (int i = 0; i < rot_dim / 2; ++i)
+    tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
+  hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
+                     rot_dim, pos0, dst_offset, eps, static_cast<float>(1.0 / static_cast<double>(d)),
+                     tab, cu_seqlens, nseq);
   return check_launch("qk_norm_rotary");
 }
 

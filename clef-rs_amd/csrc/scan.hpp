@@ -31,9 +31,19 @@ struct ScanParams {
   void* Nf;   // [chunks][Hv][4 x token blocks]            N = M (I+A)^-1 diag(beta)
   void* Ucf;  // [Hv][state tiles x token blocks]  U weighted for the capture token
   float* sc;  // [chunks][Hv][4][64]  beta, exp(gam), gam, 0
+  // Ragged batches (packed sequences, cu_seqlens): chunks never cross a
+  // sequence.  Tables built on the device by scan_tables; all null for one
+  // sequence (chunk c then spans tokens 64 c .. min(64 c + 64, T)).
+  const int* cu_seqlens;  // [nseq + 1] token offsets (device)
+  int2* chunk_tab;        // [chunks] {first token, tokens}
+  int4* seq_tab;          // [nseq] {sequence, first chunk, chunks, 0}, most chunks first
+  int* nchunk_total;      // valid entries of chunk_tab
+  int nseq;
+  int64_t init_stride;    // floats between consecutive sequences' initial states (0: shared)
 };
 
-size_t scan_workspace_bytes(int T, int Hk, int Hv, int dk, int precision);
+// nseq > 1 (or a cu_seqlens table) sizes for a ragged batch of T tokens
+size_t scan_workspace_bytes(int T, int Hk, int Hv, int dk, int precision, int nseq = 0);
 void scan_carve_workspace(ScanParams& p, void* ws, int precision);
 int scan_launch(const ScanParams& p, int precision, hipStream_t stream);
 

@@ -65,6 +65,27 @@ int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, in
                     float* captured, float* final_state, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/*
+ * Ragged batch of nseq independent sequences packed along the token axis
+ * (T tokens in total; sequence s is tokens cu_seqlens[s] .. cu_seqlens[s+1]-1,
+ * cu_seqlens a device int32 array of nseq + 1 non-decreasing offsets in
+ * [0, T]).  Each sequence runs the recurrence above from its own initial
+ * state: initial + s * initial_stride floats ([Hv, dk, dv] f32; stride 0 =
+ * one state shared by all, NULL = zero states); final_states, if not NULL,
+ * receives [nseq, Hv, dk, dv].  Layouts, dtypes and limits as above, with
+ * 1 <= nseq <= 4096; no capture.  No counterpart in the reference, which runs
+ * one request per CachedDelta call (metal.rs:340-413): this batches those
+ * calls (prefix hits resume every request from the same PrefixState).
+ */
+size_t clef_delta_scan_varlen_workspace(int T, int nseq, int Hk, int Hv, int dk, int dv, int chunk,
+                                        int precision);
+int clef_delta_scan_varlen(const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
+                           int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
+                           const int32_t* cu_seqlens, int nseq, int T, int Hk, int Hv, int dk, int dv,
+                           int chunk, int precision, const float* initial, int64_t initial_stride,
+                           void* out, int64_t so, int dtype_out, float* final_states, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Projections                                                             */
 /* ---------------------------------------------------------------------- */
@@ -116,6 +137,17 @@ int clef_conv_silu(const void* x, int64_t ldx, int dtype_in, const float* histor
                    int history_rows, const float* w, int taps, void* y, int64_t ldy, int dtype_out,
                    int T, int W, void* stream);
 /*
+ * Ragged batch of the same conv: sequence s is tokens cu_seqlens[s] ..
+ * cu_seqlens[s+1]-1 (device int32, nseq + 1 offsets) and its history rows
+ * start at history + s * history_stride floats (stride 0: one history, e.g. a
+ * shared prefix).  taps <= 8.  No counterpart in the reference (one request
+ * per call there).
+ */
+int clef_conv_silu_varlen(const void* x, int64_t ldx, int dtype_in, const float* history,
+                          int history_rows, int64_t history_stride, const int32_t* cu_seqlens, int nseq,
+                          const float* w, int taps, void* y, int64_t ldy, int dtype_out, int T, int W,
+                          void* stream);
+/*
  * Decay and write strength from the a/b projections (qwen.rs:619-627):
  * g = softplus(a + dt) * -exp(A_log) (stable softplus), beta = sigmoid(b).
  * a, b: [T, Hv] (token strides lda, ldb, dtype_in); dt, a_log: [Hv] f32;
@@ -152,6 +184,12 @@ int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int dtype_in, co
                         void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
                         int rot_dim, double theta, int pos0, int dst_offset, float eps,
                         void* stream);
+/* Ragged batch: token t of sequence s takes position pos0 + (t - cu_seqlens[s])
+ * (cu_seqlens: device int32, nseq + 1 offsets); rows stay packed. */
+int clef_qk_norm_rotary_varlen(const void* x, int64_t ldx, int64_t hs, int dtype_in, const float* w,
+                               void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
+                               int rot_dim, double theta, int pos0, const int32_t* cu_seqlens, int nseq,
+                               int dst_offset, float eps, void* stream);
 /*
  * Value layout for attention: x [T, heads, d] (token stride ldx, head stride
  * d) -> y transposed per head, [heads, d, ldy_tok] with token (dst_offset + t)
@@ -177,6 +215,24 @@ int clef_attention_gated(const void* q, int64_t ldq_tok, const void* k, int64_t 
                          const void* vt, int64_t ldv_tok, int dtype, int heads, int kv_heads,
                          int qn, int kn, int d, const void* gate, int64_t ldg, int64_t hsg,
                          void* y, int64_t ldy, void* stream);
+/*
+ * Ragged batch (mixed profile, dtype f16): sequence s owns packed rows
+ * cu_seqlens[s] .. cu_seqlens[s+1]-1 (device int32, nseq + 1 offsets in
+ * [0, T]) of q [heads, ldq_tok, d], k [kv_heads, ldk_tok, d], vt
+ * [kv_heads, d, ldv_tok], gate and y, and its queries see np prefix keys
+ * (prefix_k [kv_heads, ldpk_tok, d], prefix_vt [kv_heads, d, ldpv_tok]; all
+ * visible, np % 8 == 0, 0 with NULL buffers) before its own, causally: each
+ * sequence equals clef_attention_gated over [prefix; own] keys.  The
+ * workspace (clef_attention_varlen_workspace) holds the launch tables.  No
+ * counterpart in the reference (one request per flash-attention call there).
+ */
+size_t clef_attention_varlen_workspace(int T, int nseq);
+int clef_attention_gated_varlen(const void* q, int64_t ldq_tok, const void* k, int64_t ldk_tok,
+                                const void* vt, int64_t ldv_tok, const int32_t* cu_seqlens, int nseq, int T,
+                                const void* prefix_k, int64_t ldpk_tok, const void* prefix_vt,
+                                int64_t ldpv_tok, int np, int dtype, int heads, int kv_heads, int d,
+                                const void* gate, int64_t ldg, int64_t hsg, void* y, int64_t ldy,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Embedding gather and pooled head                                         */
@@ -253,6 +309,19 @@ size_t clef_backbone_prefix_bytes(const clef_backbone* b, int tokens);
 int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T, const void* initial,
                           int initial_tokens, int capture, void* saved, float* hidden,
                           void* workspace, size_t workspace_bytes, void* stream);
+/*
+ * Ragged batch of requests resumed from one shared prefix state (a prefix
+ * cache hit for each, prefix_cache.rs:135-177): ids is the host int32 packed
+ * token stream, cu_seqlens the host int32 offsets (cu_seqlens[0] = 0, each
+ * sequence 1..max_tokens - initial_tokens long, at most 4096 sequences and
+ * 2^20 tokens).  hidden: f32 [T, H], the final-normed hidden states of the
+ * packed tokens; sequence s's rows equal clef_backbone_prefill of its ids
+ * from `initial`.  No counterpart in the reference (one request per call).
+ */
+size_t clef_backbone_varlen_workspace(const clef_backbone* b, int T, int nseq, int prefix_tokens);
+int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids, const int32_t* cu_seqlens, int nseq,
+                                 const void* initial, int initial_tokens, float* hidden, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /*
  * Diagnostics, the counterpart of the reference's test-only `measured!`

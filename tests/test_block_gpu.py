@@ -134,3 +134,31 @@ def test_block_prefill_matches_oracle(clef, block_case, profile):
     else:
         _mixed_close(got, ref)
     assert int(np.argmax(logits)) == int(np.argmax(ref_logits))
+
+
+@gpu
+@pytest.mark.parametrize("profile", ["f32", "mixed"])
+def test_fixture_varlen_batch_equals_per_request_resume(clef, fixture, profile):
+    """A ragged batch resumed from one shared prefix state (every request a
+    prefix-cache hit, prefix_cache.rs:135-177): each request's rows equal the
+    single-request resume (qwen.rs:337-364) and the oracle over prefix + request."""
+    cfg, w, _ = fixture
+    b = clef.Backbone(cfg, _to_dev(w), profile=profile)
+    rng = np.random.default_rng(4)
+    prefix = rng.integers(0, cfg["vocab_size"], 8)
+    lens = [5, 1, 12, 3, 9]
+    reqs = [rng.integers(0, cfg["vocab_size"], n) for n in lens]
+    _, state = b.prefill(np.concatenate([prefix, reqs[0]]), capture=len(prefix))
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    hidden = b.prefill_varlen(np.concatenate(reqs), cu, initial=state).cpu().numpy()
+    orc = oracle.Backbone(cfg, w)
+    for s, ids in enumerate(reqs):
+        got = hidden[cu[s]:cu[s + 1]]
+        single = b.prefill(ids, initial=state)[0].cpu().numpy()[len(prefix):]
+        ref = orc.prefill(np.concatenate([prefix, ids]))[0][len(prefix):]
+        if profile == "f32":
+            _close(got, single, 1e-6, 1e-6)
+            _close(got, ref, 1e-5, 1e-4)
+        else:
+            _close(got, single, 2e-3, 2e-3)
+            _mixed_close(got, ref)

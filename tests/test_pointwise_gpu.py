@@ -137,3 +137,88 @@ def test_delta_gates_matches_reference_formula(clef):
     np.testing.assert_allclose(g.cpu().numpy(), (sp * -torch.exp(alog.double().cpu())).numpy(), rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(beta.cpu().numpy(), torch.sigmoid(ab[:, Hv:2 * Hv].double().cpu()).numpy(),
                                rtol=1e-6, atol=1e-7)
+
+
+@gpu
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("hist", [0, 1, 3])
+@pytest.mark.parametrize("W", [64, 12])
+def test_conv_silu_varlen_matches_per_sequence_oracle(clef, dt, hist, W):
+    """Ragged batch: each sequence is the conv of [shared history; its tokens]
+    (qwen.rs:609-618 per request); sequences of 0, 1, 2 and 3 tokens sit at
+    and inside the window's reach; W = 12 takes the any-layout kernel."""
+    lens = [40, 0, 1, 2, 3, 17, 33, 5]
+    T = sum(lens)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(11 + hist)
+    x = torch.randn((T, W), generator=gen, device="cuda").to(dt)
+    w = torch.randn((W, 1, 4), generator=gen, device="cuda") * 0.5
+    h = torch.randn((hist, W), generator=gen, device="cuda") if hist else None
+    y = clef.conv_silu_varlen(x, w, cu, history=h, out_dtype=dt)
+    got = y.float().cpu().numpy()
+    xf = x.float().cpu().numpy()
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        if a == b:
+            continue
+        full = np.concatenate([h.cpu().numpy(), xf[a:b]]) if hist else xf[a:b]
+        exp = _silu(oracle.causal_conv(full, w.cpu().numpy())[hist:].astype(np.float64))
+        if dt == torch.float32:
+            np.testing.assert_allclose(got[a:b], exp, rtol=1e-5, atol=1e-6)
+        else:
+            np.testing.assert_allclose(got[a:b], exp, rtol=2e-3, atol=1e-3)
+
+
+@gpu
+def test_qk_norm_rotary_varlen_positions(clef):
+    """Ragged batch: token t of sequence s rotates at pos0 + (t - cu[s]),
+    i.e. each sequence equals the single-sequence kernel at the same pos0."""
+    lens, heads, d, rot, pos0 = [5, 0, 12, 1], 2, 64, 32, 7
+    T = sum(lens)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    proj = torch.randn((T, heads, d), generator=gen, device="cuda")
+    w = 1.0 + 0.1 * torch.randn((d,), generator=gen, device="cuda")
+    y = clef.qk_norm_rotary_varlen(proj, heads, d, w, rot, 1e7, cu, pos0=pos0)
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        if a == b:
+            continue
+        one = clef.qk_norm_rotary(proj[a:b].contiguous(), heads, d, w, rot, 1e7, pos0=pos0)
+        torch.testing.assert_close(y[:, a:b], one, rtol=0, atol=0)
+
+
+@gpu
+@pytest.mark.parametrize("np_", [0, 64, 72])
+@pytest.mark.parametrize("d", [64, 256])
+def test_attention_varlen_matches_per_sequence_oracle(clef, np_, d):
+    """Ragged batch with a shared prefix: each sequence equals causal attention
+    over [prefix; own keys] (ops.rs:62-148, lower-right mask), gated; lengths
+    cover single tokens, tile edges and several query tiles."""
+    lens = [130, 1, 64, 300, 17, 128]
+    heads, kvh = 8, 2
+    T = sum(lens)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(np_ + d)
+    dt = torch.float16
+    q = torch.randn((heads, T, d), generator=gen, device="cuda").to(dt)
+    k = torch.randn((kvh, T, d), generator=gen, device="cuda").to(dt)
+    v = torch.randn((kvh, T, d), generator=gen, device="cuda").to(dt)
+    proj = torch.randn((T, heads, 2 * d), generator=gen, device="cuda").to(dt)
+    gate = proj[:, :, d:]
+    vt = clef.values_transposed(v.permute(1, 0, 2).contiguous().reshape(T, kvh * d), kvh, d)
+    pk = pvt = None
+    if np_:
+        pk = torch.randn((kvh, np_, d), generator=gen, device="cuda").to(dt)
+        pv = torch.randn((kvh, np_, d), generator=gen, device="cuda").to(dt)
+        pvt = clef.values_transposed(pv.permute(1, 0, 2).contiguous().reshape(np_, kvh * d), kvh, d)
+    y = clef.attention_gated_varlen(q, k, vt, gate, cu, prefix_k=pk, prefix_vt=pvt).float().cpu().numpy()
+    qf, kf, vf = (t.float().cpu().numpy() for t in (q, k, v))
+    g = gate.float().cpu().numpy()
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        ks, vs = kf[:, a:b], vf[:, a:b]
+        if np_:
+            ks = np.concatenate([pk.float().cpu().numpy(), ks], axis=1)
+            vs = np.concatenate([pv.float().cpu().numpy(), vs], axis=1)
+        att = oracle.attention(qf[:, a:b], ks, vs, True).transpose(1, 0, 2).reshape(b - a, heads * d)
+        sig = 1.0 / (1.0 + np.exp(-g[a:b].reshape(b - a, heads * d).astype(np.float64)))
+        exp = att.astype(np.float16).astype(np.float64) * sig.astype(np.float16).astype(np.float64)
+        np.testing.assert_allclose(y[a:b], exp, rtol=1e-2, atol=5e-3)

@@ -175,3 +175,35 @@ def test_scan_is_deterministic(clef):
     a = scan.prefill(q, k, v, g, beta)[0].clone()
     b = scan.prefill(q, k, v, g, beta)[0]
     assert torch.equal(a, b)
+
+
+@gpu
+@pytest.mark.parametrize("precision", ["strict", "mixed"])
+@pytest.mark.parametrize("shared", [True, False])
+def test_scan_varlen_matches_per_sequence_oracle(clef, precision, shared):
+    """Ragged batch (cu_seqlens): every sequence equals the reference recurrence
+    (qwen.rs:826-882) run alone from its own initial state; an empty sequence
+    hands its initial state through; sequences of 1, 63, 64, 65 tokens cover
+    the partial-chunk edges."""
+    lens = [200, 0, 1, 63, 64, 65, 130, 7]
+    Hk, Hv, dk, dv = 2, 4, 64, 48
+    T = sum(lens)
+    dt = torch.float32 if precision == "strict" else torch.float16
+    q, k, v, g, beta = baseline_inputs(5, T, Hk, Hv, dk, dv, dtype=dt)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    nseq = len(lens)
+    shape = (Hv, dk, dv) if shared else (nseq, Hv, dk, dv)
+    init = 0.1 * torch.randn(shape, generator=gen, device="cuda")
+    out, final = clef.DeltaScan(dk, dv, precision).prefill_varlen(q, k, v, g, beta, cu, initial=init)
+    qn, kn, vn, gn, bn = _np(q, k, v, g, beta)
+    o_all, f_all = out.cpu().numpy(), final.cpu().numpy()
+    ini = init.cpu().numpy()
+    for s, (a, b) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
+        s0 = ini if shared else ini[s]
+        if b == a:
+            np.testing.assert_array_equal(f_all[s], s0)
+            continue
+        eo, _, ef = oracle.delta_scan(qn[a:b], kn[a:b], vn[a:b], gn[a:b], bn[a:b], initial=s0)
+        _check(o_all[a:b], eo, precision)
+        _check(f_all[s], ef, precision)
