@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--cpu-tokens", type=int, default=1024,
                     help="tokens of the bounded CPU-oracle sample (0 disables it)")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--ragged", type=int, default=1,
+                    help="also time the ragged batch: 32 requests of U[128, 4096] tokens behind one shared "
+                         "512-token prefix (0: skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size reference for "
                          "HBM byte counters under rocprofv3 --pmc)")
@@ -101,6 +104,26 @@ def cpu_baseline(cfg, weights, ids, tokens, runs):
                       f"(same weights), best of {runs} runs ({sum(times):.1f} s total)"}
 
 
+def ragged_batch(model, cfg, args, torch, np, dev):
+    """32 packed requests (lengths uniform in [128, 4096], seed 4) resumed
+    from one shared 512-token prefix whose per-layer DeltaNet states, conv
+    history and attention K/V are computed once, before timing; a step is one
+    ragged prefill of all requests (cu_seqlens packing, each request with its
+    own state and causal mask)."""
+    rng = np.random.default_rng(4)
+    lens = rng.integers(128, 4097, 32)
+    prefix_ids = rng.integers(0, cfg["vocab_size"], 512)
+    req_ids = rng.integers(0, cfg["vocab_size"], int(lens.sum()))
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    _, state = model.prefill(np.concatenate([prefix_ids, req_ids[:1]]), capture=512)
+    hidden = torch.empty((int(lens.sum()), cfg["hidden_size"]), dtype=torch.float32, device=dev)
+    ms = event_ms(lambda: model.prefill_varlen(req_ids, cu, initial=state, hidden=hidden), args.steps,
+                  args.warmup, torch)
+    return {"workload": "32 requests, lengths uniform in [128, 4096] (seed 4), one shared 512-token prefix "
+                        "computed once; cu_seqlens packing", "tokens": int(lens.sum()), "prefix": 512,
+            "ms_per_step": round(ms, 4), "tok_s": round(int(lens.sum()) / (ms / 1e3), 1)}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -128,7 +151,8 @@ def main():
     cfg = workloads.block_config()
     weights = workloads.block_weights(cfg, seed=3, device=dev)
     ids = workloads.block_ids(cfg, T, seed=3).numpy()
-    model = clef_hip.Backbone(cfg, weights, profile=args.profile, max_tokens=max(4096, T))
+    # max_tokens bounds prefix + request length (the ragged batch reaches 512 + 4096)
+    model = clef_hip.Backbone(cfg, weights, profile=args.profile, max_tokens=max(8192, T))
     hidden = torch.empty((T, cfg["hidden_size"]), dtype=torch.float32, device=dev)
 
     # ---- timed region: whole prefills
@@ -197,6 +221,8 @@ def main():
         "breakdown_ms_per_step": {k: round(v["ms"], 4) for k, v in per_step.items()},
         "launches_per_step": {k: int(v["launches"]) for k, v in per_step.items()},
     }
+    if args.ragged:
+        line["ragged"] = ragged_batch(model, cfg, args, torch, np, dev)
     if args.cpu_tokens > 0:
         line["cpu_baseline"] = cpu_baseline(cfg, weights, ids, min(args.cpu_tokens, T), args.cpu_runs)
     print(json.dumps(line), flush=True)

@@ -197,6 +197,35 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
         }
     return;
   }
+  if (EPI == 1) {
+    // residual add into the f32 stream: a row block's reads are all issued
+    // before its first store (each read would otherwise wait behind the
+    // previous store, which the compiler cannot prove does not alias it)
+    float* y = static_cast<float*>(p.y);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float res[TN][16];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
+          const int c = n0 + wn * WN + j * 32 + ccol;
+          res[j][e] = (r < p.M && c < p.N) ? y[(int64_t)r * p.ldy + c] : 0.0f;
+        }
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
+          const int c = n0 + wn * WN + j * 32 + ccol;
+          const float v = acc[i][j][e];
+          if (r < p.M && c < p.N)
+            y[(int64_t)r * p.ldy + c] = res[j][e] + (p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(v)) : v);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -208,10 +237,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
         if (r < p.M && c < p.N) {
           const int64_t o = (int64_t)r * p.ldy + c;
           const float v = acc[i][j][e];
-          if (EPI == 1) {
-            float* y = static_cast<float*>(p.y);
-            y[o] = y[o] + (p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(v)) : v);
-          } else if (p.dtype_out == 1) {
+          if (p.dtype_out == 1) {
             static_cast<half_t*>(p.y)[o] = static_cast<half_t>(v);
           } else {
             static_cast<float*>(p.y)[o] = v;

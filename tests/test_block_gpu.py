@@ -162,3 +162,31 @@ def test_fixture_varlen_batch_equals_per_request_resume(clef, fixture, profile):
         else:
             _close(got, single, 2e-3, 2e-3)
             _mixed_close(got, ref)
+
+
+@gpu
+@pytest.mark.parametrize("profile", ["f32", "mixed"])
+def test_block_ragged_batch_behind_shared_prefix(clef, block_case, profile):
+    """The ragged workload at the block shape: requests packed by cu_seqlens
+    behind one 512-token prefix computed once (prefix_cache.rs:135-177), each
+    request's rows and pooled-head decision equal to its single resume
+    (qwen.rs:337-364), which the block oracle test pins."""
+    cfg, w, ids, head, _, _ = block_case
+    b = clef.Backbone(cfg, w, profile=profile, max_tokens=8192)
+    rng = np.random.default_rng(4)
+    prefix = rng.integers(0, cfg["vocab_size"], 512)
+    lens = [700, 128, 1, 65, 1500, 64]
+    reqs = [rng.integers(0, cfg["vocab_size"], n) for n in lens]
+    _, state = b.prefill(np.concatenate([prefix, reqs[0]]), capture=512)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    hidden = b.prefill_varlen(np.concatenate(reqs), cu, initial=state)
+    for s, r in enumerate(reqs):
+        single = b.prefill(r, initial=state)[0][512:]
+        got = hidden[cu[s]:cu[s + 1]]
+        if profile == "f32":
+            _close(got.cpu().numpy(), single.cpu().numpy(), 1e-5, 1e-5)
+        else:
+            _close(got.cpu().numpy(), single.cpu().numpy(), 2e-3, 2e-3)
+        lg = clef.head_logits(got[-1], head).cpu().numpy()
+        ls = clef.head_logits(single[-1], head).cpu().numpy()
+        assert int(np.argmax(lg)) == int(np.argmax(ls))
