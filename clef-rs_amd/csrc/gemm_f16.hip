@@ -51,8 +51,14 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int NB = BN * 8 / 64 / kWaves;
   typedef half8 frag;
 
-  __shared__ __attribute__((aligned(1024))) half_t sA[NS][kBM * kBK];
-  __shared__ __attribute__((aligned(1024))) half_t sB[NS][BN * kBK];
+  // NS stages of the A (256 x 64) and B (BN x 64) tiles; after the last
+  // stage the same bytes stage the accumulators for the epilogue
+  constexpr int kStA = kBM * kBK, kStB = BN * kBK;
+  __shared__ __attribute__((aligned(1024))) half_t smem[NS * (kStA + kStB)];
+  auto sA = [&](int st) { return smem + st * kStA; };
+  auto sB = [&](int st) { return smem + NS * kStA + st * kStB; };
+  static_assert(NS == 2, "two LDS stages");
+  static_assert(kWaves * 32 * WN * 4 <= (int)sizeof(smem), "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -156,7 +162,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   const int nk = p.K / kBK;
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
-    if (st < nk) issue(sA[st], sB[st], st * kBK);
+    if (st < nk) issue(sA(st), sB(st), st * kBK);
   if (NS == 3 && nk > 1)
     vm_wait<NA + NB>();
   else
@@ -166,8 +172,8 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   for (int kt = 0; kt < nk; ++kt) {
     const int nxt = cur + NS - 1 >= NS ? cur - 1 : cur + NS - 1;  // (cur + NS - 1) % NS
     const bool more = kt + NS - 1 < nk;
-    if (more) issue(sA[nxt], sB[nxt], (kt + NS - 1) * kBK);
-    compute(sA[cur], sB[cur]);
+    if (more) issue(sA(nxt), sB(nxt), (kt + NS - 1) * kBK);
+    compute(sA(cur), sB(cur));
     if (NS == 3 && more)
       vm_wait<NA + NB>();
     else
@@ -176,74 +182,99 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     cur = cur + 1 == NS ? 0 : cur + 1;
   }
 
-  // ---- epilogue.  acc[i][j][e]: row (e/4)*8 + (lane/32)*4 + e%4, col lane%32
+  // ---- epilogue.  The loop's last barrier follows every wave's last
+  // fragment read, so each wave now owns a 32 x WN f32 staging block.
+  // acc[i][j][e] holds row (e/4)*8 + (lane/32)*4 + e%4, column lane%32 of
+  // 32 x 32 block (i, j); a 32-row slab is written there and read back as
+  // 4-column chunks, so the global accesses are 8- or 16-byte vectors along
+  // the rows.  (LDS operations of one wave complete in order, so the
+  // write -> read -> next write sequence needs no barrier.)
+  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
   const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
-  if (EPI == 2) {
+  constexpr int OW = EPI == 2 ? WN / 2 : WN;  // output columns per wave
+  constexpr int CPR = OW / 4;                  // 4-column chunks per row
+  constexpr int PER = 32 * CPR / 64;           // chunks per lane per slab
+  const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
+  const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN / 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
-          const int c = n0 + wn * (WN / 2) + j * 32 + ccol;
-          if (r < p.M && c < p.N) {
-            // half roundings of neural.metal:35-42
-            const float g = static_cast<float>(static_cast<half_t>(acc[i][j][e]));
-            const float s = static_cast<float>(static_cast<half_t>(g / (1.0f + expf(-g))));
-            const float out = s * static_cast<float>(static_cast<half_t>(acc[i][j + TN / 2][e]));
-            static_cast<half_t*>(p.y)[(int64_t)r * p.ldy + c] = static_cast<half_t>(out);
-          }
-        }
-    return;
-  }
-  if (EPI == 1) {
-    // residual add into the f32 stream: a row block's reads are all issued
-    // before its first store (each read would otherwise wait behind the
-    // previous store, which the compiler cannot prove does not alias it)
-    float* y = static_cast<float*>(p.y);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      float res[TN][16];
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
-          const int c = n0 + wn * WN + j * 32 + ccol;
-          res[j][e] = (r < p.M && c < p.N) ? y[(int64_t)r * p.ldy + c] : 0.0f;
-        }
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
-          const int c = n0 + wn * WN + j * 32 + ccol;
-          const float v = acc[i][j][e];
-          if (r < p.M && c < p.N)
-            y[(int64_t)r * p.ldy + c] = res[j][e] + (p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(v)) : v);
-        }
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = m0 + wm * WM + i * 32 + (e >> 2) * 8 + rgrp + (e & 3);
-        const int c = n0 + wn * WN + j * 32 + ccol;
-        if (r < p.M && c < p.N) {
-          const int64_t o = (int64_t)r * p.ldy + c;
-          const float v = acc[i][j][e];
-          if (p.dtype_out == 1) {
-            static_cast<half_t*>(p.y)[o] = static_cast<half_t>(v);
-          } else {
-            static_cast<float*>(p.y)[o] = v;
+      for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = acc[i][j][e];
+    const int rbase = m0 + wm * WM + i * 32;
+    const int cbase = n0 + wn * OW;
+    float4 v[PER], res[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
+      if (EPI == 2) {
+        const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+        const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
+        // half roundings of neural.metal:35-42
+        auto sw = [](float gv, float uv) {
+          const float gh = static_cast<float>(static_cast<half_t>(gv));
+          const float sh = static_cast<float>(static_cast<half_t>(gh / (1.0f + expf(-gh))));
+          return sh * static_cast<float>(static_cast<half_t>(uv));
+        };
+        v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
+      } else {
+        v[q] = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+      }
+    }
+    if (EPI == 1) {
+      // residual reads all issued before the first store
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
+        const float* src = static_cast<const float*>(p.y) + (int64_t)r * p.ldy + c;
+        if (yvec && r < p.M && c + 3 < p.N) {
+          res[q] = *reinterpret_cast<const float4*>(src);
+        } else {
+          res[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (r < p.M) {
+            if (c < p.N) res[q].x = src[0];
+            if (c + 1 < p.N) res[q].y = src[1];
+            if (c + 2 < p.N) res[q].z = src[2];
+            if (c + 3 < p.N) res[q].w = src[3];
           }
         }
       }
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
+      if (r >= p.M) continue;
+      float4 o = v[q];
+      if (EPI == 1) {
+        auto rd = [&](float x) { return p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(x)) : x; };
+        o = make_float4(res[q].x + rd(o.x), res[q].y + rd(o.y), res[q].z + rd(o.z), res[q].w + rd(o.w));
+      }
+      const int64_t off = (int64_t)r * p.ldy + c;
+      if (esz == 2) {
+        half_t* dst = static_cast<half_t*>(p.y) + off;
+        const half_t h[4] = {static_cast<half_t>(o.x), static_cast<half_t>(o.y), static_cast<half_t>(o.z),
+                             static_cast<half_t>(o.w)};
+        if (yvec && c + 3 < p.N) {
+          *reinterpret_cast<half4*>(dst) = half4{h[0], h[1], h[2], h[3]};
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (c + t < p.N) dst[t] = h[t];
+        }
+      } else {
+        float* dst = static_cast<float*>(p.y) + off;
+        if (yvec && c + 3 < p.N) {
+          *reinterpret_cast<float4*>(dst) = o;
+        } else {
+          const float f[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (c + t < p.N) dst[t] = f[t];
+        }
+      }
+    }
+  }
 }
 
 template <int BN, int EPI>

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/clef_hip.h"
@@ -72,162 +73,103 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const void* x, int64_t l
   st(y, (int64_t)t * ldy + c, dto, acc / (1.0f + expf(-acc)));
 }
 
+// Eight consecutive channels of one input row, as loaded (f16 or f32).
+template <class TI>
+struct Row8;
+template <>
+struct Row8<half_t> {
+  half8 v;
+  __device__ __forceinline__ void load(const half_t* p) { v = *reinterpret_cast<const half8*>(p); }
+  __device__ __forceinline__ float at(int j) const { return static_cast<float>(v[j]); }
+};
+template <>
+struct Row8<float> {
+  float4_t a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4_t*>(p);
+    b = *reinterpret_cast<const float4_t*>(p + 4);
+  }
+  __device__ __forceinline__ float at(int j) const { return j < 4 ? a[j] : b[j - 4]; }
+};
+
+// SiLU with the hardware exp2 and reciprocal: x / (1 + e^-x) to a relative
+// error of about 1e-6 (the argument's rounding, |x| log2(e) ulp, dominates).
+__device__ __forceinline__ float silu_hw(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
+
 // Vectorised conv + SiLU: 8 consecutive channels per thread and a run of
-// kConvRun tokens, with the 3-row history window kept in registers (taps <= 4).
+// kConvRun tokens (taps <= 4; T4: taps == 4 known at compile time).  The
+// run's kConvRun + 3 input rows are all requested before the first product,
+// so a thread keeps that many 16-byte loads in flight; rows before token 0
+// come from the f32 history.  Only the first run (t0 = 0) can reach before
+// the history, so the others are compiled without the per-tap checks.
 constexpr int kConvRun = 16;
-template <class TI, class TO>
+template <class TI, class TO, bool T4>
 __global__ __launch_bounds__(256) void conv_silu_vec_kernel(const TI* __restrict__ x, int64_t ldx,
                                                             const float* __restrict__ hist, int hrows,
-                                                            const float* __restrict__ w, int taps,
+                                                            const float* __restrict__ w, int taps_rt,
                                                             TO* __restrict__ y, int64_t ldy, int T, int W) {
   const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (c0 >= W) return;
+  const int taps = T4 ? 4 : taps_rt;
   const int t0 = blockIdx.y * kConvRun;
-  float wt[8][4];
+  constexpr int R = kConvRun + 3;
+  Row8<TI> raw[R];  // raw[r]: token t0 - 3 + r
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int r = 0; r < R; ++r) {
+    const int tp = t0 - 3 + r;
+    if (tp >= 0 && tp < T) raw[r].load(x + (int64_t)tp * ldx + c0);
+  }
+  float hv[3][8];  // tokens -3..-1 (history rows hrows-3..hrows-1), zero before the history
 #pragma unroll
-    for (int k = 0; k < 4; ++k) wt[j][k] = k < taps ? w[(int64_t)(c0 + j) * taps + k] : 0.0f;
-  // window[k] holds input row (t - (taps-1) + k) of [history; x]
-  auto load_row = [&](int pos, float (&v)[8]) {  // pos: position in [history; x]
-    if (pos < 0) {
+  for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    } else if (pos < hrows) {
+    for (int j = 0; j < 8; ++j) hv[k][j] = 0.0f;
+  if (t0 == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = hist[(int64_t)pos * W + c0 + j];
-    } else {
-      const TI* src = x + (int64_t)(pos - hrows) * ldx + c0;
-      if (sizeof(TI) == 2) {
-        const half8 h = *reinterpret_cast<const half8*>(src);
+    for (int k = 0; k < 3; ++k) {
+      const int hr = hrows - 3 + k;
+      if (hr >= 0)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(h[j]);
-      } else {
-        const float4_t a = *reinterpret_cast<const float4_t*>(src);
-        const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
-      }
+        for (int j = 0; j < 8; ++j) hv[k][j] = hist[(int64_t)hr * W + c0 + j];
     }
-  };
-  float win[4][8];
-#pragma unroll
-  for (int k = 0; k < 3; ++k) load_row(hrows + t0 - 3 + k, win[k + 1]);  // rows t0-3..t0-1
-  const int t1 = min(t0 + kConvRun, T);
-  for (int t = t0; t < t1; ++t) {
-#pragma unroll
-    for (int k = 0; k < 3; ++k)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) win[k][j] = win[k + 1][j];
-    load_row(hrows + t, win[3]);
-    TO out[8];
+  }
+  // the thread's 8 x taps weights are contiguous: 16-byte loads when taps = 4
+  float wt[8][4];
+  if (taps == 4 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float acc = 0.0f;  // taps oldest -> newest, each product rounded before the add
+      const float4_t q = *reinterpret_cast<const float4_t*>(w + (int64_t)(c0 + j) * 4);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int tap = k - (4 - taps);  // window slot k holds delay 3-k
-        if (tap >= 0 && hrows + t - (3 - k) >= 0) acc = __fadd_rn(acc, __fmul_rn(win[k][j], wt[j][tap]));
-      }
-      out[j] = static_cast<TO>(acc / (1.0f + expf(-acc)));
+      for (int k = 0; k < 4; ++k) wt[j][k] = q[k];
     }
-    TO* dst = y + (int64_t)t * ldy + c0;
-    if (sizeof(TO) == 2) {
-      half8 h;
+  } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(out[j]);
-      *reinterpret_cast<half8*>(dst) = h;
-    } else {
-      float4_t a, b;
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a[j] = static_cast<float>(out[j]), b[j] = static_cast<float>(out[4 + j]);
-      *reinterpret_cast<float4_t*>(dst) = a;
-      *reinterpret_cast<float4_t*>(dst + 4) = b;
-    }
+      for (int k = 0; k < 4; ++k) wt[j][k] = k < taps ? w[(int64_t)(c0 + j) * taps + k] : 0.0f;
   }
-}
-
-// Sequence of packed token t: the last s with cu[s] <= t (cu has nseq + 1
-// entries; any table gives an index in 0..nseq-1).
-__device__ __forceinline__ int seq_of(const int* __restrict__ cu, int nseq, int t) {
-  int lo = 0, hi = nseq - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (cu[mid] <= t) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
-// Ragged batch of the vectorised conv: tokens cu[s] .. cu[s+1]-1 form sequence
-// s, whose first taps-1 inputs come from its history rows (hist + s * hs, f32
-// [hrows, W]).  A run of kConvRun tokens restarts its window at each sequence
-// start.  Rows are read only in [max(cu[s], 0), t] of the current token t.
-template <class TI, class TO>
-__global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restrict__ x, int64_t ldx,
-                                                               const float* __restrict__ hist, int hrows,
-                                                               int64_t hs, const int* __restrict__ cu, int nseq,
-                                                               const float* __restrict__ w, int taps,
-                                                               TO* __restrict__ y, int64_t ldy, int T, int W) {
-  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (c0 >= W) return;
-  const int t0 = blockIdx.y * kConvRun;
-  float wt[8][4];
+  auto run = [&](auto edge) {
+    constexpr bool EDGE = decltype(edge)::value;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) wt[j][k] = k < taps ? w[(int64_t)(c0 + j) * taps + k] : 0.0f;
-  // row tp of sequence s (first token `start`): x row, history row, or zero
-  auto load_row = [&](int s, int start, int tp, float (&v)[8]) {
-    const int hr = hrows + (tp - start);
-    if (tp >= start && tp >= 0) {
-      const TI* src = x + (int64_t)tp * ldx + c0;
-      if (sizeof(TI) == 2) {
-        const half8 h = *reinterpret_cast<const half8*>(src);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(h[j]);
-      } else {
-        const float4_t a = *reinterpret_cast<const float4_t*>(src);
-        const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
-      }
-    } else if (tp < start && hr >= 0 && hist) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = hist[(int64_t)s * hs + (int64_t)hr * W + c0 + j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    }
-  };
-  const int t1 = min(t0 + kConvRun, T);
-  int s = seq_of(cu, nseq, t0);
-  int t = t0;
-  while (t < t1) {
-    while (s + 1 < nseq && cu[s + 1] <= t) ++s;
-    const int start = cu[s];
-    const int end = s + 1 < nseq ? min(max(cu[s + 1], t + 1), t1) : t1;
-    float win[4][8];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) load_row(s, start, t - 3 + k, win[k + 1]);
-    for (; t < end; ++t) {
-#pragma unroll
-      for (int k = 0; k < 3; ++k)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) win[k][j] = win[k + 1][j];
-      load_row(s, start, t, win[3]);
-      // a delay reaches before the sequence's history: no term (as the
-      // single-sequence kernel does before row 0)
-      const int avail = hrows + (t - start);
+    for (int u = 0; u < kConvRun; ++u) {
+      const int t = t0 + u;
+      if (t >= T) break;
       TO out[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float acc = 0.0f;  // taps oldest -> newest, each product rounded before the add
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const int tap = k - (4 - taps);
-          if (tap >= 0 && avail - (3 - k) >= 0) acc = __fadd_rn(acc, __fmul_rn(win[k][j], wt[j][tap]));
+          const int tap = k - (4 - taps);  // slot k: delay 3-k, token t-3+k = raw[u + k]
+          if (tap >= 0 && (!EDGE || hrows + t - (3 - k) >= 0)) {
+            // token t-3+k < 0 only in the first run, at slots u + k < 3
+            const float v = (EDGE && u + k < 3) ? hv[u + k < 3 ? u + k : 0][j] : raw[u + k].at(j);
+            acc = __fadd_rn(acc, __fmul_rn(v, wt[j][tap]));
+          }
         }
-        out[j] = static_cast<TO>(acc / (1.0f + expf(-acc)));
+        out[j] = static_cast<TO>(silu_hw(acc));
       }
       TO* dst = y + (int64_t)t * ldy + c0;
       if (sizeof(TO) == 2) {
@@ -243,6 +185,123 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
         *reinterpret_cast<float4_t*>(dst + 4) = b;
       }
     }
+  };
+  if (t0 == 0)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
+}
+
+// Sequence of packed token t: the last s with cu[s] <= t (cu has nseq + 1
+// entries; any table gives an index in 0..nseq-1).
+__device__ __forceinline__ int seq_of(const int* __restrict__ cu, int nseq, int t) {
+  int lo = 0, hi = nseq - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Ragged batch of the vectorised conv: tokens cu[s] .. cu[s+1]-1 form sequence
+// s, whose first taps-1 inputs come from its history rows (hist + s * hs, f32
+// [hrows, W]).  The run's input rows are prefetched as in the single-sequence
+// kernel; a run whose window lies inside one sequence takes the unchecked
+// path, one that meets a sequence start resolves every tap's source (own
+// token, history row or nothing).
+template <class TI, class TO, bool T4>
+__global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restrict__ x, int64_t ldx,
+                                                               const float* __restrict__ hist, int hrows,
+                                                               int64_t hs, const int* __restrict__ cu, int nseq,
+                                                               const float* __restrict__ w, int taps_rt,
+                                                               TO* __restrict__ y, int64_t ldy, int T, int W) {
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c0 >= W) return;
+  const int taps = T4 ? 4 : taps_rt;
+  const int t0 = blockIdx.y * kConvRun;
+  const int t1 = min(t0 + kConvRun, T);
+  constexpr int R = kConvRun + 3;
+  Row8<TI> raw[R];  // raw[r]: packed token t0 - 3 + r
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int tp = t0 - 3 + r;
+    if (tp >= 0 && tp < T) raw[r].load(x + (int64_t)tp * ldx + c0);
+  }
+  float wt[8][4];
+  if (taps == 4 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4_t q = *reinterpret_cast<const float4_t*>(w + (int64_t)(c0 + j) * 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wt[j][k] = q[k];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wt[j][k] = k < taps ? w[(int64_t)(c0 + j) * taps + k] : 0.0f;
+  }
+  int s = seq_of(cu, nseq, t0);
+  const bool inside = cu[s] <= t0 - 3 && (s + 1 >= nseq || cu[s + 1] >= t1);
+  auto store = [&](int t, const float (&o)[8]) {
+    TO* dst = y + (int64_t)t * ldy + c0;
+    if (sizeof(TO) == 2) {
+      half8 h;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(o[j]);
+      *reinterpret_cast<half8*>(dst) = h;
+    } else {
+      float4_t a, b;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = o[j], b[j] = o[4 + j];
+      *reinterpret_cast<float4_t*>(dst) = a;
+      *reinterpret_cast<float4_t*>(dst + 4) = b;
+    }
+  };
+  if (inside) {
+#pragma unroll
+    for (int u = 0; u < kConvRun; ++u) {
+      if (t0 + u >= t1) break;
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float acc = 0.0f;  // taps oldest -> newest, each product rounded before the add
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int tap = k - (4 - taps);
+          if (tap >= 0) acc = __fadd_rn(acc, __fmul_rn(raw[u + k].at(j), wt[j][tap]));
+        }
+        o[j] = silu_hw(acc);
+      }
+      store(t0 + u, o);
+    }
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < kConvRun; ++u) {
+    const int t = t0 + u;
+    if (t >= t1) break;
+    while (s + 1 < nseq && cu[s + 1] <= t) ++s;
+    const int start = cu[s];
+    // a delay reaching before the sequence's history contributes no term (as
+    // the single-sequence kernel does before row 0)
+    const int avail = hrows + (t - start);
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int tap = k - (4 - taps);
+        const int tp = t - 3 + k;
+        if (tap >= 0 && avail - (3 - k) >= 0) {
+          const float v = tp >= start ? raw[u + k].at(j) : hist[(int64_t)s * hs + (int64_t)(hrows + tp - start) * W + c0 + j];
+          acc = __fadd_rn(acc, __fmul_rn(v, wt[j][tap]));
+        }
+      }
+      o[j] = silu_hw(acc);
+    }
+    store(t, o);
   }
 }
 
@@ -537,18 +596,25 @@ extern "C" int clef_conv_silu(const void* x, int64_t ldx, int dtype_in, const fl
   if (vec) {
     const dim3 g((W / 8 + 255) / 256, (T + kConvRun - 1) / kConvRun);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (dtype_in == CLEF_F16 && dtype_out == CLEF_F16)
-      hipLaunchKernelGGL((conv_silu_vec_kernel<half_t, half_t>), g, dim3(256), 0, st, static_cast<const half_t*>(x),
-                         ldx, history, history_rows, w, taps, static_cast<half_t*>(y), ldy, T, W);
-    else if (dtype_in == CLEF_F16)
-      hipLaunchKernelGGL((conv_silu_vec_kernel<half_t, float>), g, dim3(256), 0, st, static_cast<const half_t*>(x),
-                         ldx, history, history_rows, w, taps, static_cast<float*>(y), ldy, T, W);
-    else if (dtype_out == CLEF_F16)
-      hipLaunchKernelGGL((conv_silu_vec_kernel<float, half_t>), g, dim3(256), 0, st, static_cast<const float*>(x),
-                         ldx, history, history_rows, w, taps, static_cast<half_t*>(y), ldy, T, W);
-    else
-      hipLaunchKernelGGL((conv_silu_vec_kernel<float, float>), g, dim3(256), 0, st, static_cast<const float*>(x),
-                         ldx, history, history_rows, w, taps, static_cast<float*>(y), ldy, T, W);
+#define CLEF_CONV_VEC(TI, TO, T4)                                                                       \
+  hipLaunchKernelGGL((conv_silu_vec_kernel<TI, TO, T4>), g, dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
+                     history, history_rows, w, taps, static_cast<TO*>(y), ldy, T, W)
+#define CLEF_CONV_VEC_T(TI, TO)    \
+  if (taps == 4)                   \
+    CLEF_CONV_VEC(TI, TO, true);   \
+  else                             \
+    CLEF_CONV_VEC(TI, TO, false)
+    if (dtype_in == CLEF_F16 && dtype_out == CLEF_F16) {
+      CLEF_CONV_VEC_T(half_t, half_t);
+    } else if (dtype_in == CLEF_F16) {
+      CLEF_CONV_VEC_T(half_t, float);
+    } else if (dtype_out == CLEF_F16) {
+      CLEF_CONV_VEC_T(float, half_t);
+    } else {
+      CLEF_CONV_VEC_T(float, float);
+    }
+#undef CLEF_CONV_VEC_T
+#undef CLEF_CONV_VEC
     return check_launch("conv_silu");
   }
   const int64_t n = (int64_t)T * W;
@@ -580,19 +646,26 @@ extern "C" int clef_conv_silu_varlen(const void* x, int64_t ldx, int dtype_in, c
     return check_launch("conv_silu_varlen");
   }
   const dim3 g((W / 8 + 255) / 256, (T + kConvRun - 1) / kConvRun);
-#define CLEF_CONV_VL(TI, TO)                                                                                   \
-  hipLaunchKernelGGL((conv_silu_varlen_kernel<TI, TO>), g, dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
-                     history, history_rows, history_stride, cu_seqlens, nseq, w, taps, static_cast<TO*>(y), ldy, \
+#define CLEF_CONV_VL4(TI, TO, T4)                                                                              \
+  hipLaunchKernelGGL((conv_silu_varlen_kernel<TI, TO, T4>), g, dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
+                     history, history_rows, history_stride, cu_seqlens, nseq, w, taps, static_cast<TO*>(y), ldy,     \
                      T, W)
-  if (dtype_in == CLEF_F16 && dtype_out == CLEF_F16)
+#define CLEF_CONV_VL(TI, TO)      \
+  if (taps == 4)                  \
+    CLEF_CONV_VL4(TI, TO, true);  \
+  else                            \
+    CLEF_CONV_VL4(TI, TO, false)
+  if (dtype_in == CLEF_F16 && dtype_out == CLEF_F16) {
     CLEF_CONV_VL(half_t, half_t);
-  else if (dtype_in == CLEF_F16)
+  } else if (dtype_in == CLEF_F16) {
     CLEF_CONV_VL(half_t, float);
-  else if (dtype_out == CLEF_F16)
+  } else if (dtype_out == CLEF_F16) {
     CLEF_CONV_VL(float, half_t);
-  else
+  } else {
     CLEF_CONV_VL(float, float);
+  }
 #undef CLEF_CONV_VL
+#undef CLEF_CONV_VL4
   return check_launch("conv_silu_varlen");
 }
 

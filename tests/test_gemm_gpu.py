@@ -62,7 +62,7 @@ def test_gemm_projection_shapes(clef, N, dtype):
 
 
 @gpu
-@pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8)])
+@pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8), (300, 203, 128)])
 def test_gemm_residual_epilogue(clef, M, N, K):
     x, w = _inputs(3, M, N, K, torch.float16)
     h = torch.randn((M, N), device="cuda")
@@ -73,6 +73,21 @@ def test_gemm_residual_epilogue(clef, M, N, K):
     err = (h - exp).abs()  # one half ulp of the product, plus the f32 add
     assert (err <= 1e-3 + prod.abs() * 2.0 ** -10 + exp.abs() * 2.0 ** -23).all(), \
         f"max err {err.max().item():.3e}"
+
+
+@gpu
+@pytest.mark.parametrize("M,N,K", [(512, 256, 256), (300, 203, 128)])
+def test_gemm_residual_epilogue_unrounded(clef, M, N, K):
+    """Residual add of the f32 accumulator itself (no half rounding), aligned
+    and ragged rows."""
+    x, w = _inputs(8, M, N, K, torch.float16)
+    h = torch.randn((M, N), device="cuda")
+    h0 = h.clone()
+    clef.gemm(x, w, residual=h, out_dtype=torch.float32)
+    prod = x.double() @ w.double().T
+    scale = x.double().abs() @ w.double().abs().T
+    err = (h.double() - (h0.double() + prod)).abs()
+    assert (err <= 1e-5 * scale + 2e-6 * (h0.double().abs() + 1)).all(), f"max err {err.max().item():.3e}"
 
 
 @gpu
