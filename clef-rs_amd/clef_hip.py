@@ -55,6 +55,9 @@ SIGNATURES = {
     "clef_rms_norm": (_i, [_p, _l, _i, _p, _p, _l, _i, _i, _i, _f, _p]),
     "clef_conv_silu": (_i, [_p, _l, _i, _p, _i, _p, _i, _p, _l, _i, _i, _i, _p]),
     "clef_delta_gates": (_i, [_p, _l, _p, _l, _i, _p, _p, _p, _p, _i, _i, _p]),
+    "clef_delta_gates_pack_bytes": (_z, [_i, _i]),
+    "clef_delta_gates_pack": (_i, [_p, _l, _i, _i, _i, _p, _p]),
+    "clef_delta_gates_proj": (_i, [_p, _l, _p, _i, _i, _p, _p, _p, _p, _i, _i, _p]),
     "clef_attention_varlen_workspace": (_z, [_i, _i]),
     "clef_attention_gated_varlen": (_i, [_p, _l, _p, _l, _p, _l, _p, _i, _i, _p, _l, _p, _l, _i, _i, _i, _i, _i,
                                          _p, _l, _l, _p, _l, _p, _z, _p]),
@@ -311,6 +314,28 @@ def delta_gates(a, b, dt, a_log):
     beta = torch.empty_like(g)
     _check(lib().clef_delta_gates(_ptr(a), _rows(a, "a"), _ptr(b), _rows(b, "b"), _dt(a), _ptr(dt),
                                   _ptr(a_log), _ptr(g), _ptr(beta), T, Hv, _stream()))
+    return g, beta
+
+
+def delta_gates_pack(w_ab):
+    """w_ab [2 Hv, K] f16 in the fragment order clef_delta_gates_proj reads."""
+    K = w_ab.shape[1]
+    Hv = w_ab.shape[0] // 2
+    n = lib().clef_delta_gates_pack_bytes(K, Hv)
+    if n == 0:
+        raise ClefError(-1, "gates projection dimensions")
+    packed = torch.empty(n, dtype=torch.uint8, device=w_ab.device)
+    _check(lib().clef_delta_gates_pack(_ptr(w_ab), _rows(w_ab, "w_ab"), K, Hv, _dt(w_ab), _ptr(packed), _stream()))
+    return packed
+
+
+def delta_gates_proj(x, packed, Hv, dt, a_log):
+    """[a | b] = x w_ab^T (f16, each rounded to f16) and the gates in one launch."""
+    T, K = x.shape
+    g = torch.empty((T, Hv), dtype=torch.float32, device=x.device)
+    beta = torch.empty_like(g)
+    _check(lib().clef_delta_gates_proj(_ptr(x), _rows(x, "x"), _ptr(packed), K, _dt(x), _ptr(dt), _ptr(a_log),
+                                       _ptr(g), _ptr(beta), T, Hv, _stream()))
     return g, beta
 
 

@@ -40,6 +40,7 @@ struct LayerState {
   int kind = 0;
   // owned
   void* in_w = nullptr;        // fused [qkv | z | a | b] or [q | k | v], act dtype
+  void* ab_packed = nullptr;   // [a | b] rows in fragment order (clef_delta_gates_pack)
   float* in_norm = nullptr;    // input_norm offset
   float* post_norm = nullptr;  // post_attention_layernorm offset
   float* conv = nullptr;       // [W, taps]
@@ -75,6 +76,9 @@ struct clef_backbone {
   int ad = CLEF_F32;      // activation / projection dtype
   int conv_dt = CLEF_F32; // dtype of the conv output fed to the scan
   int key = 0, value = 0, W = 0, NP = 0, NA = 0;  // widths
+  // f16 profile: the a/b projections run fused with the gates
+  // (clef_delta_gates_proj), so the in-projection GEMM covers [qkv | z] only
+  bool ab_fused = false;
 };
 
 namespace clef {
@@ -285,6 +289,8 @@ extern "C" int clef_backbone_create(const clef_backbone_config* config, const cl
   b->value = C.lin_v_heads * C.lin_dv;
   b->W = 2 * b->key + b->value;
   b->NP = b->W + b->value + 2 * C.lin_v_heads;
+  b->ab_fused = C.profile == CLEF_PROFILE_MIXED_F16 &&
+                (C.lin_v_heads == 16 || C.lin_v_heads == 32 || C.lin_v_heads == 64) && C.hidden % 256 == 0;
   b->NA = 2 * C.heads * C.head_dim + 2 * C.kv_heads * C.head_dim;
   b->embeddings = embeddings;
   const size_t a = elt(b->ad);
@@ -334,6 +340,13 @@ extern "C" int clef_backbone_create(const clef_backbone_config* config, const cl
         o += a * (size_t)rows * H;
       }
       S.in_w = w;
+      if (b->ab_fused) {
+        S.ab_packed = alloc(clef_delta_gates_pack_bytes(H, C.lin_v_heads));
+        if (!S.ab_packed) return cleanup(), fail(-2, "backbone: device allocation failed");
+        if (int rc = clef_delta_gates_pack(w + a * (size_t)(b->W + b->value) * H, H, H, C.lin_v_heads, CLEF_F16,
+                                           S.ab_packed, nullptr))
+          return cleanup(), rc;
+      }
       S.out = L.out;
       S.conv = offset_norm(L.conv, b->W * C.conv_taps, 0.0f);
       S.dt = offset_norm(L.dt, C.lin_v_heads, 0.0f);
@@ -456,16 +469,22 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
       char* proj = static_cast<char*>(w.proj);
-      TIMED(CLEF_CAT_GEMM, 2.0 * T * NP * H, gemm_bytes(T, NP, H, false),
-            clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NP, H, ad, ad, CLEF_EPI_STORE, s));
+      const int NG = b->ab_fused ? Wc + b->value : NP;  // GEMM columns
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * NG * H, gemm_bytes(T, NG, H, false),
+            clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NG, H, ad, ad, CLEF_EPI_STORE, s));
       const int hist_rows = initial ? (offset < taps - 1 ? offset : taps - 1) : 0;
       const double ce = static_cast<double>(elt(b->conv_dt));
       TIMED(CLEF_CAT_CONV, 2.0 * T * Wc * taps, (da + ce) * T * Wc,
             clef_conv_silu(proj, NP, ad, initial ? init.hist[li] : nullptr, hist_rows, L.conv, taps, w.mixed, Wc,
                            b->conv_dt, T, Wc, s));
-      TIMED(CLEF_CAT_OTHER, 0, (2.0 * da + 8.0) * T * Hv,
-            clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt, L.a_log,
-                             w.g, w.beta, T, Hv, s));
+      if (b->ab_fused) {
+        TIMED(CLEF_CAT_OTHER, 2.0 * T * 2 * Hv * H, da * (T * H + 2.0 * Hv * H) + 8.0 * T * Hv,
+              clef_delta_gates_proj(w.n, H, L.ab_packed, H, ad, L.dt, L.a_log, w.g, w.beta, T, Hv, s));
+      } else {
+        TIMED(CLEF_CAT_OTHER, 0, (2.0 * da + 8.0) * T * Hv,
+              clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt,
+                               L.a_log, w.g, w.beta, T, Hv, s));
+      }
       const char* mixed = static_cast<const char*>(w.mixed);
       const size_t ces = elt(b->conv_dt);
       const double nchunk = (T + 63) / 64;
@@ -605,16 +624,22 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
       char* proj = static_cast<char*>(w.proj);
-      TIMED(CLEF_CAT_GEMM, 2.0 * T * NP * H, gemm_bytes(T, NP, H, false),
-            clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NP, H, ad, ad, CLEF_EPI_STORE, s));
+      const int NG = b->ab_fused ? Wc + b->value : NP;  // GEMM columns
+      TIMED(CLEF_CAT_GEMM, 2.0 * T * NG * H, gemm_bytes(T, NG, H, false),
+            clef_gemm(w.n, H, L.in_w, H, proj, NP, T, NG, H, ad, ad, CLEF_EPI_STORE, s));
       const int hist_rows = initial ? (offset < taps - 1 ? offset : taps - 1) : 0;
       const double ce = static_cast<double>(elt(b->conv_dt));
       TIMED(CLEF_CAT_CONV, 2.0 * T * Wc * taps, (da + ce) * T * Wc,
             clef_conv_silu_varlen(proj, NP, ad, initial ? init.hist[li] : nullptr, hist_rows, 0, w.cu, nseq,
                                   L.conv, taps, w.mixed, Wc, b->conv_dt, T, Wc, s));
-      TIMED(CLEF_CAT_OTHER, 0, (2.0 * da + 8.0) * T * Hv,
-            clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt, L.a_log,
-                             w.g, w.beta, T, Hv, s));
+      if (b->ab_fused) {
+        TIMED(CLEF_CAT_OTHER, 2.0 * T * 2 * Hv * H, da * (T * H + 2.0 * Hv * H) + 8.0 * T * Hv,
+              clef_delta_gates_proj(w.n, H, L.ab_packed, H, ad, L.dt, L.a_log, w.g, w.beta, T, Hv, s));
+      } else {
+        TIMED(CLEF_CAT_OTHER, 0, (2.0 * da + 8.0) * T * Hv,
+              clef_delta_gates(proj + a * (Wc + b->value), NP, proj + a * (Wc + b->value + Hv), NP, ad, L.dt,
+                               L.a_log, w.g, w.beta, T, Hv, s));
+      }
       const char* mixed = static_cast<const char*>(w.mixed);
       const size_t ces = elt(b->conv_dt);
       const double state = 4.0 * Hv * c.lin_dk * dv;

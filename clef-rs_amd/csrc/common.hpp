@@ -73,6 +73,16 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// DeltaNet gates (qwen.rs:615-623): decay g = softplus(a + dt) * -exp(A_log)
+// with the stable softplus max(x, 0) + log(1 + exp(-|x|)), strength
+// beta = sigmoid(b); f32 throughout, each step rounded as written.
+__device__ __forceinline__ float delta_decay(float a, float dt, float alog) {
+  const float av = __fadd_rn(a, dt);
+  const float sp = __fadd_rn(fmaxf(av, 0.0f), logf(__fadd_rn(expf(-fabsf(av)), 1.0f)));
+  return __fmul_rn(sp, -expf(alog));
+}
+__device__ __forceinline__ float delta_strength(float b) { return 1.0f / (1.0f + expf(-b)); }
+
 // ---- host-side error plumbing ---------------------------------------------
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);  // records msg, returns code

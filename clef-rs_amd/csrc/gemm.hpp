@@ -24,4 +24,11 @@ int gemm_launch(const GemmParams& p, int epilogue, hipStream_t stream);
 bool gemm_f16_dma_ok(const GemmParams& p);
 int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t stream);
 
+// a/b projections fused with the DeltaNet gates (gemm_f16.hip); f16 operands,
+// Hv in {16, 32, 64}, K % 256 == 0, K <= 4096, rows 16-byte aligned (checked
+// by the caller).  The weights are first packed into MFMA fragment order.
+int ab_pack_f16_launch(const void* w_ab, int64_t ldw, int K, int Hv, void* packed, hipStream_t stream);
+int ab_gates_f16_launch(const void* x, int64_t ldx, const void* packed, int K, const float* dt, const float* a_log,
+                        float* g, float* beta, int T, int Hv, hipStream_t stream);
+
 }  // namespace clef

@@ -13,6 +13,8 @@
 // c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit 16
 // distinct bank groups.  The DMA lanes pick their source chunk so that the
 // lane-ordered LDS writes produce that layout.
+#include <algorithm>
+
 #include "common.hpp"
 #include "gemm.hpp"
 
@@ -287,7 +289,143 @@ int launch(const GemmParams& p, hipStream_t s) {
   return check_launch("gemm");
 }
 
+// w_ab [2 Hv, K] in MFMA fragment order: k-step s (32 columns), output block
+// j (16 rows), lane l, element e hold w_ab[16 j + l % 16][32 s + 8 (l / 16) + e],
+// so a wave reads one block's fragment as 1 KiB of consecutive bytes.
+__global__ void ab_pack_f16(const half_t* __restrict__ w, int64_t ldw, int K, int no, half8* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (s, j, lane)
+  const int nb = no / 16;
+  if (idx >= (int64_t)(K / 32) * nb * 64) return;
+  const int lane = static_cast<int>(idx % 64), j = static_cast<int>((idx / 64) % nb);
+  const int st = static_cast<int>(idx / (64 * nb));
+  out[idx] = *reinterpret_cast<const half8*>(w + (int64_t)(16 * j + lane % 16) * ldw + 32 * st + 8 * (lane / 16));
+}
+
+// [a | b] = x . w_ab^T and the DeltaNet gates for 16 tokens per work-group of
+// 16 waves (v_mfma_f32_16x16x32_f16).  The tokens' x rows go to LDS once, with
+// row-contiguous 16-byte loads, the 16-byte column chunk c of row r stored at
+// c ^ (r & 7); wave q then takes the k-steps q, q + 16, ..., its x fragments
+// from LDS and its w_ab fragments straight from the packed copy (1 KiB per
+// load, L2-resident), and the 16 partial sums meet in LDS in a fixed order
+// (a token's result does not depend on its position in the batch).  With 16
+// waves a group has its whole share of loads in flight at once.
+// (Fragments read from row-major global memory would touch 16 rows per
+// instruction, which leaves the address unit the bottleneck.)  Each output is
+// rounded to f16 as the reference's separate a and b projections store it
+// (qwen.rs:612-623), then turned into the decay or the strength.
+template <int HV>
+__global__ __launch_bounds__(1024) void ab_gates_f16(const half_t* __restrict__ x, int64_t ldx,
+                                                    const half8* __restrict__ wpk, int K,
+                                                    const float* __restrict__ dt, const float* __restrict__ alog,
+                                                    float* __restrict__ g, float* __restrict__ beta, int T) {
+  constexpr int NB = 2 * HV / 16;  // 16-output blocks
+  constexpr int NW = 16;           // waves
+  extern __shared__ __attribute__((aligned(16))) half_t sx[];  // [16][K], then the partial sums
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.x * 16;
+  const int nsteps = K / 32;
+  constexpr int U = 16 / NB;  // k-steps per batch of w_ab loads (16 loads)
+  half8 b[U][NB];
+  auto load_b = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (s0 + NW * u < nsteps)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) b[u][j] = wpk[((int64_t)(s0 + NW * u) * NB + j) * 64 + lane];
+  };
+  load_b(wave);  // independent of x: in flight while x is staged
+  // x: 512-byte row segments, 32 threads each; K / 256 segments per row
+  {
+    const int spr = K / 256, nseg = 16 * spr, l32 = tid & 31;
+    constexpr int XB = 4;  // segments per thread in flight together
+    for (int s0 = tid >> 5; s0 < nseg; s0 += 32 * XB) {
+      half8 v[XB];
+#pragma unroll
+      for (int i = 0; i < XB; ++i) {
+        const int sg = s0 + 32 * i;
+        if (sg < nseg) {
+          const int r = sg / spr, c = (sg % spr) * 32 + l32;
+          v[i] = *reinterpret_cast<const half8*>(x + (int64_t)min(t0 + r, T - 1) * ldx + c * 8);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < XB; ++i) {
+        const int sg = s0 + 32 * i;
+        if (sg < nseg) {
+          const int r = sg / spr, c = (sg % spr) * 32 + l32;
+          *reinterpret_cast<half8*>(sx + r * K + ((c ^ (r & 7)) << 3)) = v[i];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  float4_t acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // fragment lane layout: row lane % 16, k 8 (lane / 16) .. + 7 of the k-step
+  const int fr = lane & 15, fg = lane >> 4;
+  for (int s0 = wave; s0 < nsteps; s0 += NW * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int st = s0 + NW * u;
+      if (st < nsteps) {
+        const int c = 4 * st + fg;
+        const half8 a = *reinterpret_cast<const half8*>(sx + fr * K + ((c ^ (fr & 7)) << 3));
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[u][j], acc[j], 0, 0, 0);
+      }
+    }
+    if (s0 + NW * U < nsteps) load_b(s0 + NW * U);
+  }
+  __syncthreads();  // x no longer read: its LDS holds the partial sums
+  float4_t* part = reinterpret_cast<float4_t*>(sx);  // [NW][NB][64]
+#pragma unroll
+  for (int j = 0; j < NB; ++j) part[(wave * NB + j) * 64 + lane] = acc[j];
+  __syncthreads();
+  // block j's sums, row r: token t0 + 4 (lane / 16) + r, output 16 j + lane % 16
+  if (wave >= NB) return;
+  const int j = wave;
+  float4_t v4 = part[j * 64 + lane];
+  for (int q = 1; q < NW; ++q) v4 += part[(q * NB + j) * 64 + lane];
+  const int n = j * 16 + fr;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + 4 * fg + r;
+    if (t >= T) continue;
+    const float v = static_cast<float>(static_cast<half_t>(v4[r]));
+    if (n < HV)
+      g[(int64_t)t * HV + n] = delta_decay(v, dt[n], alog[n]);
+    else
+      beta[(int64_t)t * HV + n - HV] = delta_strength(v);
+  }
+}
+
 }  // namespace
+
+int ab_pack_f16_launch(const void* w_ab, int64_t ldw, int K, int Hv, void* packed, hipStream_t s) {
+  const int64_t n = (int64_t)(K / 32) * (2 * Hv / 16) * 64;
+  hipLaunchKernelGGL(ab_pack_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const half_t*>(w_ab), ldw, K, 2 * Hv, static_cast<half8*>(packed));
+  return check_launch("delta_gates_pack");
+}
+
+int ab_gates_f16_launch(const void* x, int64_t ldx, const void* packed, int K, const float* dt, const float* a_log,
+                        float* g, float* beta, int T, int Hv, hipStream_t s) {
+  const dim3 grid((T + 15) / 16);
+  // 16 rows of x (f16), reused for the 16 x (2 Hv / 16) x 1 KiB partial sums
+  const size_t lds = std::max((size_t)32 * K, (size_t)16 * (2 * Hv / 16) * 1024);
+  auto X = static_cast<const half_t*>(x);
+  auto P = static_cast<const half8*>(packed);
+  if (Hv == 16)
+    hipLaunchKernelGGL(ab_gates_f16<16>, grid, dim3(1024), lds, s, X, ldx, P, K, dt, a_log, g, beta, T);
+  else if (Hv == 32)
+    hipLaunchKernelGGL(ab_gates_f16<32>, grid, dim3(1024), lds, s, X, ldx, P, K, dt, a_log, g, beta, T);
+  else if (Hv == 64)
+    hipLaunchKernelGGL(ab_gates_f16<64>, grid, dim3(1024), lds, s, X, ldx, P, K, dt, a_log, g, beta, T);
+  else
+    return fail(-1, "gates projection: Hv must be 16, 32 or 64");
+  return check_launch("delta_gates_proj");
+}
 
 bool gemm_f16_dma_ok(const GemmParams& p) {
   return p.dtype_in == 1 && p.vec && p.M >= kBM && p.K % kBK == 0 &&

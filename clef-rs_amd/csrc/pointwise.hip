@@ -425,10 +425,8 @@ __global__ __launch_bounds__(256) void gates_kernel(const void* a, int64_t lda, 
   const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx >= T * Hv) return;
   const int t = idx / Hv, h = idx % Hv;
-  const float av = __fadd_rn(ld(a, (int64_t)t * lda + h, dti), dt[h]);
-  const float sp = __fadd_rn(fmaxf(av, 0.0f), logf(__fadd_rn(expf(-fabsf(av)), 1.0f)));
-  g[idx] = __fmul_rn(sp, -expf(alog[h]));
-  beta[idx] = 1.0f / (1.0f + expf(-ld(b, (int64_t)t * ldb + h, dti)));
+  g[idx] = delta_decay(ld(a, (int64_t)t * lda + h, dti), dt[h], alog[h]);
+  beta[idx] = delta_strength(ld(b, (int64_t)t * ldb + h, dti));
 }
 
 // ---- gated output norm (qwen.rs:671-676): one wave per (token, head) row ----

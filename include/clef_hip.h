@@ -157,6 +157,23 @@ int clef_delta_gates(const void* a, int64_t lda, const void* b, int64_t ldb, int
                      const float* dt, const float* a_log, float* g, float* beta, int T, int Hv,
                      void* stream);
 /*
+ * The a/b projections and the gates in one launch (f16 operands): [a | b] =
+ * x . w_ab^T with f32 accumulation, each value rounded to f16 as the
+ * reference's separate in_proj_a / in_proj_b projections store it
+ * (qwen.rs:612-623), then g and beta as clef_delta_gates.  w_ab: [2 Hv, K]
+ * (row stride ldw), rows 0..Hv-1 in_proj_a and Hv..2Hv-1 in_proj_b, packed
+ * once by clef_delta_gates_pack into a device buffer of
+ * clef_delta_gates_pack_bytes(K, Hv) bytes (MFMA fragment order; 16-byte
+ * aligned).  x: [T, K] (row stride ldx); g, beta: [T, Hv] f32.  Hv in
+ * {16, 32, 64}, K a multiple of 256 up to 4096, rows 16-byte aligned.  Lets
+ * the in-projection GEMM cover [qkv | z] only (a whole number of 256-column
+ * tiles).
+ */
+size_t clef_delta_gates_pack_bytes(int K, int Hv);
+int clef_delta_gates_pack(const void* w_ab, int64_t ldw, int K, int Hv, int dtype, void* packed, void* stream);
+int clef_delta_gates_proj(const void* x, int64_t ldx, const void* packed, int K, int dtype, const float* dt,
+                          const float* a_log, float* g, float* beta, int T, int Hv, void* stream);
+/*
  * Gated output norm, qwen.rs:671-676: per token and v-head row of `width`,
  * o is rounded to dtype_out (the scan output cast to the activation dtype),
  * RMS-normalised in f32 with w (no offset), rounded to dtype_out, multiplied

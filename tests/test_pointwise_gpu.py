@@ -140,6 +140,25 @@ def test_delta_gates_matches_reference_formula(clef):
 
 
 @gpu
+@pytest.mark.parametrize("T,K,Hv", [(4096, 2048, 32), (333, 256, 16), (1, 512, 64), (17, 2048, 32)])
+def test_delta_gates_proj_matches_projection_then_gates(clef, T, K, Hv):
+    """The fused a/b projections + gates equal the in-projection GEMM's a/b
+    columns (f16) followed by the gates kernel: the two f32 accumulation
+    orders may round a value to the neighbouring half, nothing more."""
+    gen = torch.Generator(device="cuda").manual_seed(T + K)
+    x = torch.randn((T, K), generator=gen, device="cuda").half()
+    w_ab = (torch.randn((2 * Hv, K), generator=gen, device="cuda") * 0.05).half()
+    dt = torch.randn(Hv, generator=gen, device="cuda")
+    alog = torch.randn(Hv, generator=gen, device="cuda")
+    g, beta = clef.delta_gates_proj(x, clef.delta_gates_pack(w_ab), Hv, dt, alog)
+    ab = clef.gemm(x, w_ab)
+    g0, beta0 = clef.delta_gates(ab[:, :Hv], ab[:, Hv:], dt, alog)
+    for got, ref in ((g, g0), (beta, beta0)):
+        assert (got == ref).float().mean().item() > 0.99
+        np.testing.assert_allclose(got.cpu().numpy(), ref.cpu().numpy(), rtol=1e-2, atol=1e-3)
+
+
+@gpu
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
 @pytest.mark.parametrize("hist", [0, 1, 3])
 @pytest.mark.parametrize("W", [64, 12])
