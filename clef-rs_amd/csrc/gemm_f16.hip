@@ -432,14 +432,38 @@ bool gemm_f16_dma_ok(const GemmParams& p) {
          (int64_t)p.M * p.ldx < (int64_t(1) << 31);
 }
 
-// 256 x 256 tiles unless that leaves most of the 256 CUs idle
+// CUs of the current device (cached per device)
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Tile width: one 256 x BN tile per CU at a time (the LDS holds one), so a
+// launch takes ceil(tiles / CUs) rounds, each as long as a tile; a narrower
+// tile costs a little more per column (fewer products per fragment read and
+// per byte moved).  The width with the least rounds x width x that cost wins,
+// e.g. 256 for N = 12288, 192 for N = 9216 (768 tiles: 3 full rounds instead
+// of 2.25), 128 for N = 2048 (256 tiles: one round).  SwiGLU keeps 256 or 128
+// (its wave columns pair gate and up blocks).
 int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t s) {
   const int n_eff = epilogue == 2 ? 2 * p.N : p.N;
-  const long tiles256 = (long)((p.M + kBM - 1) / kBM) * ((n_eff + 255) / 256);
-  const bool wide = tiles256 >= 384;
-  if (epilogue == 0) return wide ? launch<256, 0>(p, s) : launch<128, 0>(p, s);
-  if (epilogue == 1) return wide ? launch<256, 1>(p, s) : launch<128, 1>(p, s);
-  return wide ? launch<256, 2>(p, s) : launch<128, 2>(p, s);
+  const long tm = (p.M + kBM - 1) / kBM, cus = device_cus();
+  auto cost = [&](int bn, double per_col) {
+    const long tiles = tm * ((n_eff + bn - 1) / bn);
+    return (double)((tiles + cus - 1) / cus) * bn * per_col;
+  };
+  const double c256 = cost(256, 1.0), c192 = epilogue == 2 ? 1e300 : cost(192, 1.1), c128 = cost(128, 1.2);
+  const int bn = c256 <= c192 && c256 <= c128 ? 256 : (c192 <= c128 ? 192 : 128);
+  if (epilogue == 0) return bn == 256 ? launch<256, 0>(p, s) : bn == 192 ? launch<192, 0>(p, s) : launch<128, 0>(p, s);
+  if (epilogue == 1) return bn == 256 ? launch<256, 1>(p, s) : bn == 192 ? launch<192, 1>(p, s) : launch<128, 1>(p, s);
+  return bn == 256 ? launch<256, 2>(p, s) : launch<128, 2>(p, s);
 }
 
 }  // namespace clef

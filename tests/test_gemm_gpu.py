@@ -38,7 +38,8 @@ def _check_f32(y, x, w):
     assert (err <= 1e-5 * scale + 1e-6).all(), f"max rel err {(err / (scale + 1e-30)).max().item():.3e}"
 
 
-SHAPES = [(1, 1, 1), (17, 73, 65), (139, 129, 128), (17, 73, 4096), (513, 137, 65), (1025, 257, 128)]
+SHAPES = [(1, 1, 1), (17, 73, 65), (139, 129, 128), (17, 73, 4096), (513, 137, 65), (1025, 257, 128),
+          (4096, 3000, 256)]  # the last: 192-wide tiles, ragged last column
 
 
 @gpu
@@ -52,7 +53,7 @@ def test_gemm_reference_shapes(clef, M, N, K, dtype):
 
 
 @gpu
-@pytest.mark.parametrize("N", [8192, 2048, 6144, 12352])
+@pytest.mark.parametrize("N", [8192, 2048, 6144, 12352, 9216])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_gemm_projection_shapes(clef, N, dtype):
     """M = 2048 tokens, K = 2048 hidden; x ~ N(0,1), W ~ N(0,0.02), seed 1."""
@@ -62,7 +63,8 @@ def test_gemm_projection_shapes(clef, N, dtype):
 
 
 @gpu
-@pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8), (300, 203, 128)])
+@pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8), (300, 203, 128),
+                                   (4096, 3000, 256)])
 def test_gemm_residual_epilogue(clef, M, N, K):
     x, w = _inputs(3, M, N, K, torch.float16)
     h = torch.randn((M, N), device="cuda")
