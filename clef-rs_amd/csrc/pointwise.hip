@@ -495,6 +495,95 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int6
   }
 }
 
+// One token per work-group (four waves, heads h = wave, wave + 4, ...), each
+// lane holding EPL = d / 64 consecutive features: the rotation's cos and sin
+// are computed once per token and frequency (shared by every head, as the
+// pair i, i + rot/2 shares its angle), rows are read and written as vectors,
+// and a rotated feature's partner comes from the lane rot / (2 EPL) away.
+// Same per-element roundings as qk_norm_rotary_kernel; the squares are
+// summed per lane over consecutive features, then across the wave.
+template <int EPL, class TI, class TO>
+__global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__ x, int64_t ldx, int64_t hs,
+                                                          const float* __restrict__ w, TO* __restrict__ y,
+                                                          int64_t ldy_tok, int heads, int rot, int pos0,
+                                                          int dst_offset, float eps, float inv_width, int vec,
+                                                          RotaryTable tab, const int* __restrict__ cu, int nseq) {
+  constexpr int D = 64 * EPL;
+  __shared__ float cs[128], sn[128];
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = rot / 2;
+  // position: pos0 + t, or pos0 + (t - first token of t's sequence)
+  const float p = static_cast<float>(pos0 + (cu ? t - cu[seq_of(cu, nseq, t)] : t));
+  for (int f = threadIdx.x; f < half; f += 256) {
+    const float ang = __fmul_rn(p, tab.inv_freq[f]);
+    cs[f] = cosf(ang);
+    sn[f] = sinf(ang);
+  }
+  __syncthreads();
+  const int i0 = lane * EPL;
+  const int pd = half / EPL;  // partner lane distance
+  float wv[EPL], cw[EPL], sw[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int i = i0 + e;
+    wv[e] = w[i];
+    const int f = i < half ? i : i - half;
+    cw[e] = i < rot ? cs[f] : 1.0f;
+    sw[e] = i < rot ? (i < half ? -sn[f] : sn[f]) : 0.0f;  // r = -v[i + half] below half, v[i - half] above
+  }
+  for (int h = wave; h < heads; h += 4) {
+    const TI* src = x + (int64_t)t * ldx + (int64_t)h * hs + i0;
+    float v[EPL];
+    bool got = false;
+    if constexpr (EPL == 4) {
+      if (vec) {
+        if constexpr (sizeof(TI) == 2) {
+          const half4 q = *reinterpret_cast<const half4*>(src);
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) v[e] = static_cast<float>(q[e]);
+        } else {
+          const float4_t q = *reinterpret_cast<const float4_t*>(src);
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) v[e] = q[e];
+        }
+        got = true;
+      }
+    }
+    if (!got)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) v[e] = static_cast<float>(src[e]);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) ss += v[e] * v[e];
+    ss = wave_sum(ss);
+    const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(ss, inv_width), eps));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      v[e] = static_cast<float>(static_cast<TO>(__fmul_rn(__fmul_rn(v[e], inverse), wv[e])));
+    const int plane = i0 < half ? lane + pd : (i0 < rot ? lane - pd : lane);
+    TO out[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float vj = __shfl(v[e], plane, 64);
+      out[e] = static_cast<TO>(i0 + e < rot ? __fadd_rn(__fmul_rn(v[e], cw[e]), __fmul_rn(vj, sw[e])) : v[e]);
+    }
+    TO* dst = y + ((int64_t)h * ldy_tok + dst_offset + t) * D + i0;
+    bool done = false;
+    if constexpr (EPL == 4) {
+      if (vec) {
+        if constexpr (sizeof(TO) == 2)
+          *reinterpret_cast<half4*>(dst) = half4{out[0], out[1], out[2], out[3]};
+        else
+          *reinterpret_cast<float4_t*>(dst) = float4_t{out[0], out[1], out[2], out[3]};
+        done = true;
+      }
+    }
+    if (!done)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) dst[e] = out[e];
+  }
+}
+
 // ---- values to [heads, d, tokens] --------------------------------------------
 __global__ __launch_bounds__(256) void values_t_kernel(const void* x, int64_t ldx, int dti, void* y,
                                                        int64_t ldy_tok, int dto, int T, int heads,
@@ -711,6 +800,44 @@ extern "C" int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, i
   return check_launch("gated_rms_silu");
 }
 
+// per-token kernel when d is 64, 128 or 256 and the rotary half splits into
+// whole lanes; false if not taken (nothing launched)
+static bool qk_norm_rotary_tok_launch(const void* x, int64_t ldx, int64_t hs, int dti, const float* w, void* y,
+                                      int64_t ldy_tok, int dto, int T, int heads, int d, int rot, int pos0,
+                                      int dst_offset, float eps, const RotaryTable& tab, const int* cu, int nseq,
+                                      hipStream_t st) {
+  const int epl = d / 64;
+  if (d % 64 != 0 || !(epl == 1 || epl == 2 || epl == 4) || (rot / 2) % epl != 0) return false;
+  const int es_in = dti == CLEF_F16 ? 2 : 4, es_out = dto == CLEF_F16 ? 2 : 4;
+  const int vec = (reinterpret_cast<uintptr_t>(x) % (es_in * epl) == 0 && (ldx * es_in) % (es_in * epl) == 0 &&
+                   (hs * es_in) % (es_in * epl) == 0 && reinterpret_cast<uintptr_t>(y) % (es_out * epl) == 0)
+                      ? 1
+                      : 0;
+  const float inv = static_cast<float>(1.0 / static_cast<double>(d));
+#define CLEF_QKR(E, TI, TO)                                                                                     \
+  hipLaunchKernelGGL((qk_norm_rotary_tok<E, TI, TO>), dim3(T), dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
+                     hs, w, static_cast<TO*>(y), ldy_tok, heads, rot, pos0, dst_offset, eps, inv, vec, tab, cu, nseq)
+#define CLEF_QKR_E(TI, TO)      \
+  if (epl == 4)                 \
+    CLEF_QKR(4, TI, TO);        \
+  else if (epl == 2)            \
+    CLEF_QKR(2, TI, TO);        \
+  else                          \
+    CLEF_QKR(1, TI, TO)
+  if (dti == CLEF_F16 && dto == CLEF_F16) {
+    CLEF_QKR_E(half_t, half_t);
+  } else if (dti == CLEF_F16) {
+    CLEF_QKR_E(half_t, float);
+  } else if (dto == CLEF_F16) {
+    CLEF_QKR_E(float, half_t);
+  } else {
+    CLEF_QKR_E(float, float);
+  }
+#undef CLEF_QKR_E
+#undef CLEF_QKR
+  return true;
+}
+
 extern "C" int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int dtype_in, const float* w,
                                    void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
                                    int rot_dim, double theta, int pos0, int dst_offset, float eps,
@@ -727,6 +854,9 @@ extern "C" int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int d
   RotaryTable tab{};
   for (int i = 0; i < rot_dim / 2; ++i)  // ops.rs:165: theta.powf(-(2i)/dim) in f64, then f32
     tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
+  if (qk_norm_rotary_tok_launch(x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d, rot_dim, pos0,
+                                dst_offset, eps, tab, nullptr, 0, static_cast<hipStream_t>(stream)))
+    return check_launch("qk_norm_rotary");
   hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
                      rot_dim, pos0, dst_offset, eps, static_cast<float>(1.0 / static_cast<double>(d)),
@@ -750,6 +880,9 @@ extern "C" int clef_qk_norm_rotary_varlen(const void* x, int64_t ldx, int64_t hs
   RotaryTable tab{};
   for (int i = 0; i < rot_dim / 2; ++i)
     tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
+  if (qk_norm_rotary_tok_launch(x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d, rot_dim, pos0,
+                                dst_offset, eps, tab, cu_seqlens, nseq, static_cast<hipStream_t>(stream)))
+    return check_launch("qk_norm_rotary");
   hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
                      rot_dim, pos0, dst_offset, eps, static_cast<float>(1.0 / static_cast<double>(d)),

@@ -109,8 +109,11 @@ def test_attention_gated_matches_oracle(clef, heads, kvh, qn, kn, d, dt):
 
 @gpu
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
-def test_qk_norm_rotary_matches_oracle(clef, dt):
-    T, heads, d, rot, pos0 = 37, 4, 256, 64, 11
+@pytest.mark.parametrize("heads,d,rot,pos0", [(4, 256, 64, 11), (5, 128, 64, 4000), (3, 64, 32, 0), (2, 96, 32, 5)])
+def test_qk_norm_rotary_matches_oracle(clef, dt, heads, d, rot, pos0):
+    """d = 64, 128, 256: one token per work-group, lanes of 1, 2, 4 features;
+    d = 96: one wave per (token, head); pos0 = 4000 reaches large angles."""
+    T = 37
     gen = torch.Generator(device="cuda").manual_seed(1)
     proj = torch.randn((T, heads, 2 * d), generator=gen, device="cuda").to(dt)
     w = 1.0 + 0.1 * torch.randn((d,), generator=gen, device="cuda")
