@@ -452,7 +452,7 @@ static int device_cus() {
 // e.g. 256 for N = 12288, 192 for N = 9216 (768 tiles: 3 full rounds instead
 // of 2.25), 128 for N = 2048 (256 tiles: one round).  SwiGLU keeps 256 or 128
 // (its wave columns pair gate and up blocks).
-int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t s) {
+int gemm_f16_tile_width(const GemmParams& p, int epilogue) {
   const int n_eff = epilogue == 2 ? 2 * p.N : p.N;
   const long tm = (p.M + kBM - 1) / kBM, cus = device_cus();
   auto cost = [&](int bn, double per_col) {
@@ -460,7 +460,11 @@ int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t s) {
     return (double)((tiles + cus - 1) / cus) * bn * per_col;
   };
   const double c256 = cost(256, 1.0), c192 = epilogue == 2 ? 1e300 : cost(192, 1.1), c128 = cost(128, 1.2);
-  const int bn = c256 <= c192 && c256 <= c128 ? 256 : (c192 <= c128 ? 192 : 128);
+  return c256 <= c192 && c256 <= c128 ? 256 : (c192 <= c128 ? 192 : 128);
+}
+
+int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t s) {
+  const int bn = gemm_f16_tile_width(p, epilogue);
   if (epilogue == 0) return bn == 256 ? launch<256, 0>(p, s) : bn == 192 ? launch<192, 0>(p, s) : launch<128, 0>(p, s);
   if (epilogue == 1) return bn == 256 ? launch<256, 1>(p, s) : bn == 192 ? launch<192, 1>(p, s) : launch<128, 1>(p, s);
   return bn == 256 ? launch<256, 2>(p, s) : launch<128, 2>(p, s);

@@ -113,6 +113,22 @@ int clef_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
  */
 int clef_gemm_swiglu(const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
                      void* y, int64_t ldy, int M, int N, int K, int dtype, void* stream);
+/*
+ * The same projections with the weights packed once (f16 only): a loader
+ * that owns its weights packs each projection into MFMA fragment order
+ * (clef_gemm_pack, into clef_gemm_pack_bytes(N, K) bytes of device memory,
+ * 16-byte aligned), and the packed GEMM then reads every weight fragment as
+ * consecutive bytes straight into registers, leaving the LDS to the
+ * activations.  K must be a multiple of 64.  clef_gemm_packed: as clef_gemm,
+ * epilogues CLEF_EPI_STORE and CLEF_EPI_RESIDUAL with the same roundings
+ * (SwiGLU: clef_gemm_swiglu).  Extends the reference's GemmKernel
+ * (neural.rs:50-58), whose weights stay row-major; clef_gemm remains the
+ * drop-in entry point.
+ */
+size_t clef_gemm_pack_bytes(int N, int K);
+int clef_gemm_pack(const void* w, int64_t ldw, int N, int K, int dtype, void* packed, void* stream);
+int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, void* y, int64_t ldy, int M, int N, int K,
+                     int dtype_in, int dtype_out, int epilogue, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Pointwise pieces around the scan                                        */

@@ -134,3 +134,48 @@ def test_swiglu_f32(clef):
     g = x.double() @ wg.double().T
     ref = torch.nn.functional.silu(g) * (x.double() @ wu.double().T)
     assert (y.double() - ref).abs().max().item() < 1e-4
+
+
+@gpu
+@pytest.mark.parametrize("M,N,K", [(4096, 12288, 2048), (4096, 9216, 2048), (2048, 2048, 4096), (300, 203, 128),
+                                   (1025, 257, 192), (1, 64, 64), (777, 3000, 320)])
+def test_packed_weights_match_row_major_gemm(clef, M, N, K):
+    """Packed-weight GEMM: the same k-ordered MFMA accumulation as the
+    row-major f16 kernel (bit-identical where that kernel runs, M >= 256),
+    and within one half ulp of the f32 product everywhere."""
+    x, w = _inputs(9, M, N, K, torch.float16)
+    pw = clef.PackedWeights(w)
+    y = clef.gemm_packed(x, pw)
+    _check_f16(y, x, w)
+    if M >= 256:
+        assert torch.equal(y, clef.gemm(x, w))
+    y32 = clef.gemm_packed(x, pw, out_dtype=torch.float32)
+    assert torch.equal(y32.half(), y)
+    h = torch.randn((M, N), device="cuda")
+    h_ref = h.clone()
+    clef.gemm_packed(x, pw, residual=h, out_dtype=torch.float16)
+    clef.gemm(x, w, residual=h_ref, out_dtype=torch.float16) if M >= 256 else h_ref.add_(y.float())
+    assert torch.equal(h, h_ref)
+
+
+@gpu
+@pytest.mark.skip(reason="the packed SwiGLU epilogue faulted the GPU at M=513, N=137, K=64 with no cause found "
+                         "on the CPU; the path is switched off (clef_gemm_packed rejects it) until one is")
+@pytest.mark.parametrize("M,N,K", [(2048, 6144, 2048), (600, 6144, 2048), (513, 137, 64)])
+def test_packed_swiglu_matches_row_major(clef, M, N, K):
+    gen = torch.Generator(device="cuda").manual_seed(15)
+    x = torch.randn((M, K), generator=gen, device="cuda").half()
+    wg = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    wu = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    # the withdrawn form (gate and up rows packed in alternating groups of 64);
+    # kept as the record of the case that faulted
+    y = clef.gemm_packed(x, clef.PackedWeights(wg, wu))
+    assert torch.equal(y, clef.gemm_swiglu(x, wg, wu))
+
+
+def test_packed_gemm_rejects_swiglu(clef):
+    """The packed path takes store and residual epilogues only."""
+    import ctypes
+    rc = clef.lib().clef_gemm_packed(ctypes.c_void_p(16), 64, ctypes.c_void_p(16), ctypes.c_void_p(16), 64, 4, 4,
+                                     64, 1, 1, 2, None)
+    assert rc != 0
