@@ -595,6 +595,11 @@ class Backbone:
         return {name: {"ms": ms[i], "launches": cnt[i], "flops": fl[i], "bytes": by[i]}
                 for i, name in enumerate(CATEGORIES)}
 
+    @classmethod
+    def from_safetensors(cls, config: dict, paths, profile: str = "f32", **kw):
+        """Backbone whose weights come from safetensors shards (load_backbone_weights)."""
+        return cls(config, load_backbone_weights(config, paths, profile), profile=profile, **kw)
+
     def prefix_bytes(self, tokens):
         return lib().clef_backbone_prefix_bytes(self._h, tokens)
 
@@ -643,6 +648,138 @@ class Backbone:
             _ptr(initial.buffer) if initial is not None else None, prefix, _ptr(hidden), _ptr(self._ws),
             self._ws.numel(), _stream()))
         return hidden
+
+
+# ---------------------------------------------------------------------------
+# Weights on disk (models/weights.rs:26-104)
+# ---------------------------------------------------------------------------
+SIGNATURES.update({
+    "clef_st_open": (_i, [C.c_char_p, C.POINTER(_p)]),
+    "clef_st_close": (None, [_p]),
+    "clef_st_count": (_i, [_p]),
+    "clef_st_info": (_i, [_p, _i, C.POINTER(C.c_char_p), C.POINTER(_i), C.POINTER(_i), C.POINTER(_l)]),
+    "clef_st_find": (_i, [_p, C.c_char_p]),
+    "clef_st_load": (_i, [_p, _i, _i, _p, _z, _p]),
+})
+_ST_NAMES = {0: "F32", 1: "F16", 2: "BF16"}
+
+
+class SafeTensors:
+    """A safetensors file opened and validated by the native reader."""
+
+    def __init__(self, path):
+        L = lib()
+        _declare(L)
+        h = _p()
+        _check(L.clef_st_open(str(path).encode(), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().clef_st_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self, i):
+        name, dt, rank = C.c_char_p(), _i(), _i()
+        shape = (_l * 8)()
+        _check(lib().clef_st_info(self._h, i, C.byref(name), C.byref(dt), C.byref(rank), shape))
+        return name.value.decode(), _ST_NAMES[dt.value], tuple(shape[d] for d in range(rank.value))
+
+    def tensors(self):
+        """{name: (dtype, shape)} of every tensor in the file."""
+        out = {}
+        for i in range(lib().clef_st_count(self._h)):
+            name, dt, shape = self.info(i)
+            out[name] = (dt, shape)
+        return out
+
+    def load(self, name, dtype=torch.float32, device=None):
+        """The tensor on the device, converted there to f16 or f32."""
+        i = lib().clef_st_find(self._h, name.encode())
+        if i < 0:
+            raise ClefError(-1, f"safetensors: no tensor {name}")
+        _, _, shape = self.info(i)
+        dev = device or torch.device("cuda", torch.cuda.current_device())
+        t = torch.empty(shape, dtype=dtype, device=dev)
+        _check(lib().clef_st_load(self._h, i, _DT[dtype], _ptr(t), t.numel() * t.element_size(), _stream()))
+        return t
+
+
+def backbone_tensor_specs(config: dict):
+    """{checkpoint name: (shape, 'mat' | 'vec')} the hybrid backbone consumes
+    (qwen.rs:193-310, 540-586 names and shapes)."""
+    P = Backbone.P
+    H, I = config["hidden_size"], config["intermediate_size"]
+    specs = {P + "embed_tokens.weight": ((config["vocab_size"], H), "mat"), P + "norm.weight": ((H,), "vec")}
+    key = config["linear_num_key_heads"] * config["linear_key_head_dim"]
+    value = config["linear_num_value_heads"] * config["linear_value_head_dim"]
+    hv, taps = config["linear_num_value_heads"], config["linear_conv_kernel_dim"]
+    heads, kvh, d = config["num_attention_heads"], config["num_key_value_heads"], config["head_dim"]
+    for i, kind in enumerate(config["layer_types"]):
+        p = f"{P}layers.{i}."
+        specs[p + "input_layernorm.weight"] = ((H,), "vec")
+        specs[p + "post_attention_layernorm.weight"] = ((H,), "vec")
+        specs[p + "mlp.gate_proj.weight"] = ((I, H), "mat")
+        specs[p + "mlp.up_proj.weight"] = ((I, H), "mat")
+        specs[p + "mlp.down_proj.weight"] = ((H, I), "mat")
+        if kind == "full_attention":
+            a = p + "self_attn."
+            specs[a + "q_proj.weight"] = ((2 * heads * d, H), "mat")
+            specs[a + "k_proj.weight"] = ((kvh * d, H), "mat")
+            specs[a + "v_proj.weight"] = ((kvh * d, H), "mat")
+            specs[a + "o_proj.weight"] = ((H, heads * d), "mat")
+            specs[a + "q_norm.weight"] = ((d,), "vec")
+            specs[a + "k_norm.weight"] = ((d,), "vec")
+        else:
+            a = p + "linear_attn."
+            specs[a + "in_proj_qkv.weight"] = ((2 * key + value, H), "mat")
+            specs[a + "in_proj_z.weight"] = ((value, H), "mat")
+            specs[a + "in_proj_a.weight"] = ((hv, H), "mat")
+            specs[a + "in_proj_b.weight"] = ((hv, H), "mat")
+            specs[a + "out_proj.weight"] = ((H, value), "mat")
+            specs[a + "conv1d.weight"] = ((2 * key + value, 1, taps), "vec")
+            specs[a + "dt_bias"] = ((hv,), "vec")
+            specs[a + "A_log"] = ((hv,), "vec")
+            specs[a + "norm.weight"] = ((config["linear_value_head_dim"],), "vec")
+    return specs
+
+
+def load_backbone_weights(config: dict, paths, profile: str = "f32", device=None):
+    """Backbone weights from safetensors shards, as Weights::load checks them
+    (weights.rs:26-104): every required tensor present once with its shape,
+    no unconsumed tensor under the language-model prefix (weights.rs:184-189;
+    other namespaces, e.g. a vision tower, are skipped), matrices converted
+    on the device to the profile's dtype and vectors to f32."""
+    specs = backbone_tensor_specs(config)
+    mat_dtype = torch.float32 if profile == "f32" else torch.float16
+    out = {}
+    for path in ([paths] if isinstance(paths, (str, bytes)) or hasattr(paths, "__fspath__") else paths):
+        with SafeTensors(path) as st:
+            for name, (_, shape) in st.tensors().items():
+                if name not in specs:
+                    if name.startswith(Backbone.P):
+                        raise ClefError(-1, f"weights: unconsumed model tensor {name}")
+                    continue
+                want, kind = specs[name]
+                if tuple(shape) != tuple(want) or name in out:
+                    raise ClefError(-1, f"weights: tensor shape or duplicate {name}")
+                out[name] = st.load(name, mat_dtype if kind == "mat" else torch.float32, device)
+    missing = [n for n in specs if n not in out]
+    if missing:
+        raise ClefError(-1, f"weights: missing required tensor {missing[0]}")
+    return out
 
 
 def head_logits(x_row, w):

@@ -370,6 +370,32 @@ int clef_backbone_enable_timing(clef_backbone* b, int enable);
 int clef_backbone_timings(clef_backbone* b, double* ms, int* launches, double* flops,
                           double* bytes);
 
+/* ---------------------------------------------------------------------- */
+/* Weights on disk                                                         */
+/* ---------------------------------------------------------------------- */
+/*
+ * Safetensors reader and device loader (the reference's Weights::load and
+ * validate_header, models/weights.rs:26-104, 196-215).  clef_st_open maps a
+ * file read-only and validates its header before returning: header length
+ * at most 1 MiB, a JSON object of at most 2048 entries without duplicate
+ * names, dtypes BF16 / F16 / F32, byte lengths equal to the shapes, and
+ * tensors tiling the data section exactly; any violation is an error and no
+ * handle is returned.  clef_st_info / clef_st_find describe the tensors
+ * (name valid while the handle is open; shape8 receives up to 8 dims).
+ * clef_st_load copies tensor i to the device and converts it there into
+ * dtype_out (CLEF_F16 or CLEF_F32; BF16 -> F32 is exact, -> F16 rounds to
+ * nearest even), using one tensor's worth of staging; it returns when the
+ * data is in place.  The handle owns the mapping until clef_st_close.
+ */
+enum { CLEF_ST_BF16 = 2, CLEF_ST_F16 = 1, CLEF_ST_F32 = 0 };
+typedef struct clef_safetensors clef_safetensors;
+int clef_st_open(const char* path, clef_safetensors** out);
+void clef_st_close(clef_safetensors* f);
+int clef_st_count(const clef_safetensors* f);
+int clef_st_info(const clef_safetensors* f, int i, const char** name, int* dtype, int* rank, int64_t* shape8);
+int clef_st_find(const clef_safetensors* f, const char* name);
+int clef_st_load(const clef_safetensors* f, int i, int dtype_out, void* dst, size_t dst_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
