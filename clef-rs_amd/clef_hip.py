@@ -67,7 +67,7 @@ SIGNATURES = {
     "clef_conv_silu_varlen": (_i, [_p, _l, _i, _p, _i, _l, _p, _i, _p, _i, _p, _l, _i, _i, _i, _p]),
     "clef_qk_norm_rotary_varlen": (_i, [_p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _d, _i, _p, _i, _i, _f,
                                         _p]),
-    "clef_gated_rms_silu": (_i, [_p, _p, _l, _i, _p, _p, _i, _i, _i, _i, _f, _p]),
+    "clef_gated_rms_silu": (_i, [_p, _i, _p, _l, _i, _p, _p, _i, _i, _i, _i, _f, _p]),
     "clef_qk_norm_rotary": (_i, [_p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _d, _i, _i, _f, _p]),
     "clef_values_transposed": (_i, [_p, _l, _i, _p, _l, _i, _i, _i, _i, _i, _p]),
     "clef_attention_gated": (_i, [_p, _l, _p, _l, _p, _l, _i, _i, _i, _i, _i, _i, _p, _l, _l, _p, _l,
@@ -375,7 +375,7 @@ def delta_gates_proj(x, packed, Hv, dt, a_log):
 def gated_rms_silu(o, z, w, eps=1e-6, out_dtype=torch.float32):
     T, Hv, width = o.shape
     y = torch.empty((T, Hv * width), dtype=out_dtype, device=o.device)
-    _check(lib().clef_gated_rms_silu(_ptr(o), _ptr(z), z.stride(0), _dt(z), _ptr(w), _ptr(y), _dt(y),
+    _check(lib().clef_gated_rms_silu(_ptr(o), _dt(o), _ptr(z), z.stride(0), _dt(z), _ptr(w), _ptr(y), _dt(y),
                                      T, Hv, width, float(eps), _stream()))
     return y
 

@@ -106,7 +106,7 @@ struct Workspace {
   void* mixed;    // [T, W] conv_dt
   float* g;       // [T, Hv]
   float* beta;    // [T, Hv]
-  float* scan_out;  // [T, Hv*dv]
+  void* scan_out;   // [T, Hv*dv] in the activation dtype
   void* gated;    // [T, max(value, heads*d)] act
   void* mlp;      // [T, I] act
   void* qh;       // [heads, T, d] act
@@ -155,7 +155,7 @@ size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base
   W.mixed = take(elt(b->conv_dt) * T * b->W);
   W.g = static_cast<float*>(take(4ull * T * c.lin_v_heads));
   W.beta = static_cast<float*>(take(4ull * T * c.lin_v_heads));
-  W.scan_out = static_cast<float*>(take(4ull * T * b->value));
+  W.scan_out = take(4ull * T * b->value);
   W.gated = take(a * T * gated_cols);
   W.mlp = take(a * T * c.intermediate);
   W.qh = take(a * (size_t)c.heads * T * c.head_dim);
@@ -492,15 +492,17 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
           nchunk * (c.lin_k_heads * 4.0 * 64 * 64 * c.lin_dk +
                     Hv * (2.0 * 64 * 64 * c.lin_dk + 4.0 * 64 * 64 * dv + 6.0 * 64 * c.lin_dk * dv + 64.0 * 64 * 64 * 2 / 3));
       const double state = 4.0 * Hv * c.lin_dk * dv;
-      const double scan_bytes = ce * T * (2.0 * b->key + b->value) + 8.0 * T * Hv + 4.0 * T * b->value +
+      // the scan writes o in the activation dtype: the gated norm rounds it
+      // there first (qwen.rs:671), so f16 output is the same value
+      const double scan_bytes = ce * T * (2.0 * b->key + b->value) + 8.0 * T * Hv + da * T * b->value +
                                 (initial ? state : 0.0) + (capture ? state : 0.0);
       TIMED(CLEF_CAT_SCAN, scan_flops, scan_bytes,
             clef_delta_scan(mixed, mixed + ces * b->key, mixed + ces * 2 * b->key, Wc, Wc, b->conv_dt, w.g, w.beta, Hv,
                             CLEF_F32, T, c.lin_k_heads, Hv, c.lin_dk, dv, 64, c.scan_precision,
-                            initial ? init.rec[li] : nullptr, capture, w.scan_out, (int64_t)Hv * dv, CLEF_F32,
+                            initial ? init.rec[li] : nullptr, capture, w.scan_out, (int64_t)Hv * dv, ad,
                             capture ? sav.rec[li] : nullptr, nullptr, w.scan_ws, w.scan_ws_bytes, s));
-      TIMED(CLEF_CAT_NORM, 6.0 * T * b->value, (4.0 + 2.0 * da) * T * b->value,
-            clef_gated_rms_silu(w.scan_out, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
+      TIMED(CLEF_CAT_NORM, 6.0 * T * b->value, 3.0 * da * T * b->value,
+            clef_gated_rms_silu(w.scan_out, ad, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
       TIMED(CLEF_CAT_GEMM, 2.0 * T * H * b->value, gemm_bytes(T, H, b->value, true),
             clef_gemm(w.gated, b->value, L.out, b->value, h, H, T, H, b->value, ad, ad, CLEF_EPI_RESIDUAL, s));
       if (capture) {  // conv history: last min(capture, taps-1) projected rows (qwen.rs:677-685)
@@ -643,15 +645,15 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
       const char* mixed = static_cast<const char*>(w.mixed);
       const size_t ces = elt(b->conv_dt);
       const double state = 4.0 * Hv * c.lin_dk * dv;
-      const double scan_bytes = ce * T * (2.0 * b->key + b->value) + 8.0 * T * Hv + 4.0 * T * b->value +
+      const double scan_bytes = ce * T * (2.0 * b->key + b->value) + 8.0 * T * Hv + da * T * b->value +
                                 (initial ? state : 0.0);
       TIMED(CLEF_CAT_SCAN, 0, scan_bytes,
             clef_delta_scan_varlen(mixed, mixed + ces * b->key, mixed + ces * 2 * b->key, Wc, Wc, b->conv_dt, w.g,
                                    w.beta, Hv, CLEF_F32, w.cu, nseq, T, c.lin_k_heads, Hv, c.lin_dk, dv, 64,
                                    c.scan_precision, initial ? init.rec[li] : nullptr, 0, w.scan_out,
-                                   (int64_t)Hv * dv, CLEF_F32, nullptr, w.scan_ws, w.scan_ws_bytes, s));
-      TIMED(CLEF_CAT_NORM, 6.0 * T * b->value, (4.0 + 2.0 * da) * T * b->value,
-            clef_gated_rms_silu(w.scan_out, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
+                                   (int64_t)Hv * dv, ad, nullptr, w.scan_ws, w.scan_ws_bytes, s));
+      TIMED(CLEF_CAT_NORM, 6.0 * T * b->value, 3.0 * da * T * b->value,
+            clef_gated_rms_silu(w.scan_out, ad, proj + a * Wc, NP, ad, L.gnorm, w.gated, ad, T, Hv, dv, c.eps, s));
       TIMED(CLEF_CAT_GEMM, 2.0 * T * H * b->value, gemm_bytes(T, H, b->value, true),
             clef_gemm(w.gated, b->value, L.out, b->value, h, H, T, H, b->value, ad, ad, CLEF_EPI_RESIDUAL, s));
     } else {

@@ -70,6 +70,34 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// f32 multiply and add, each rounded on its own.  HIP's __fmul_rn and
+// __fadd_rn are plain operators, which the compiler still contracts into an
+// FMA or folds into a following f16 conversion (v_fma_mixlo_f16: one rounding
+// where the reference rounds twice); contraction is off inside these.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
+// f32 -> f16, round to nearest even, of the f32 value as rounded.  The empty
+// asm keeps the compiler from folding a producing multiply into the
+// conversion (v_fma_mixlo_f16 rounds the exact product once).
+__device__ __forceinline__ half_t to_f16(float x) {
+  asm("" : "+v"(x));
+  return static_cast<half_t>(x);
+}
+template <class T>
+__device__ __forceinline__ T cvt_out(float x) {
+  if constexpr (sizeof(T) == 2)
+    return to_f16(x);
+  else
+    return x;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -77,9 +105,9 @@ __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-
 // with the stable softplus max(x, 0) + log(1 + exp(-|x|)), strength
 // beta = sigmoid(b); f32 throughout, each step rounded as written.
 __device__ __forceinline__ float delta_decay(float a, float dt, float alog) {
-  const float av = __fadd_rn(a, dt);
-  const float sp = __fadd_rn(fmaxf(av, 0.0f), logf(__fadd_rn(expf(-fabsf(av)), 1.0f)));
-  return __fmul_rn(sp, -expf(alog));
+  const float av = add_rn(a, dt);
+  const float sp = add_rn(fmaxf(av, 0.0f), logf(add_rn(expf(-fabsf(av)), 1.0f)));
+  return mul_rn(sp, -expf(alog));
 }
 __device__ __forceinline__ float delta_strength(float b) { return 1.0f / (1.0f + expf(-b)); }
 

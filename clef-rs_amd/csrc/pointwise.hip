@@ -1,8 +1,8 @@
 // Memory-bound pieces around the scan and the attention core, with their C ABI
 // entry points.  Each kernel keeps the reference's op order and rounding
 // points (crates/core/src/models/qwen.rs, ops.rs, pointwise.metal); the
-// multiply/add pairs that the reference rounds separately use __fmul_rn /
-// __fadd_rn so the compiler cannot contract them into FMAs.
+// multiplies and adds that the reference rounds separately use mul_rn /
+// add_rn, inside which the compiler may not contract or fold roundings.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -23,10 +23,10 @@ __device__ __forceinline__ void st(void* p, int64_t i, int dtype, float v) {
   if (dtype == CLEF_F32)
     static_cast<float*>(p)[i] = v;
   else
-    static_cast<half_t*>(p)[i] = static_cast<half_t>(v);
+    static_cast<half_t*>(p)[i] = to_f16(v);
 }
 __device__ __forceinline__ float rnd(float v, int dtype) {
-  return dtype == CLEF_F16 ? static_cast<float>(static_cast<half_t>(v)) : v;
+  return dtype == CLEF_F16 ? static_cast<float>(to_f16(v)) : v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -47,10 +47,10 @@ __global__ __launch_bounds__(256) void rms_kernel(const void* x, int64_t ldx, in
     s += v * v;
   }
   s = wave_sum(s);
-  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, inv_width), eps));
   for (int i = lane; i < width; i += 64) {
     const float v = ld(x, (int64_t)row * ldx + i, dti);
-    st(y, (int64_t)row * ldy + i, dto, __fmul_rn(__fmul_rn(v, inverse), w[i]));
+    st(y, (int64_t)row * ldy + i, dto, mul_rn(mul_rn(v, inverse), w[i]));
   }
 }
 
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const void* x, int64_t l
     const int src = pos - (taps - 1 - tap);
     if (src < 0) continue;
     const float v = src < hrows ? hist[(int64_t)src * W + c] : ld(x, (int64_t)(src - hrows) * ldx + c, dti);
-    acc = __fadd_rn(acc, __fmul_rn(v, w[(int64_t)c * taps + tap]));
+    acc = add_rn(acc, mul_rn(v, w[(int64_t)c * taps + tap]));
   }
   st(y, (int64_t)t * ldy + c, dto, acc / (1.0f + expf(-acc)));
 }
@@ -166,16 +166,16 @@ __global__ __launch_bounds__(256) void conv_silu_vec_kernel(const TI* __restrict
           if (tap >= 0 && (!EDGE || hrows + t - (3 - k) >= 0)) {
             // token t-3+k < 0 only in the first run, at slots u + k < 3
             const float v = (EDGE && u + k < 3) ? hv[u + k < 3 ? u + k : 0][j] : raw[u + k].at(j);
-            acc = __fadd_rn(acc, __fmul_rn(v, wt[j][tap]));
+            acc = add_rn(acc, mul_rn(v, wt[j][tap]));
           }
         }
-        out[j] = static_cast<TO>(silu_hw(acc));
+        out[j] = cvt_out<TO>(silu_hw(acc));
       }
       TO* dst = y + (int64_t)t * ldy + c0;
       if (sizeof(TO) == 2) {
         half8 h;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(out[j]);
+        for (int j = 0; j < 8; ++j) h[j] = to_f16(out[j]);
         *reinterpret_cast<half8*>(dst) = h;
       } else {
         float4_t a, b;
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
     if (sizeof(TO) == 2) {
       half8 h;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(o[j]);
+      for (int j = 0; j < 8; ++j) h[j] = to_f16(o[j]);
       *reinterpret_cast<half8*>(dst) = h;
     } else {
       float4_t a, b;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int tap = k - (4 - taps);
-          if (tap >= 0) acc = __fadd_rn(acc, __fmul_rn(raw[u + k].at(j), wt[j][tap]));
+          if (tap >= 0) acc = add_rn(acc, mul_rn(raw[u + k].at(j), wt[j][tap]));
         }
         o[j] = silu_hw(acc);
       }
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
         const int tp = t - 3 + k;
         if (tap >= 0 && avail - (3 - k) >= 0) {
           const float v = tp >= start ? raw[u + k].at(j) : hist[(int64_t)s * hs + (int64_t)(hrows + tp - start) * W + c0 + j];
-          acc = __fadd_rn(acc, __fmul_rn(v, wt[j][tap]));
+          acc = add_rn(acc, mul_rn(v, wt[j][tap]));
         }
       }
       o[j] = silu_hw(acc);
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_scalar(const void* x, in
       v = hist[(int64_t)s * hs + (int64_t)hr * W + c];
     else
       continue;
-    acc = __fadd_rn(acc, __fmul_rn(v, w[(int64_t)c * taps + tap]));
+    acc = add_rn(acc, mul_rn(v, w[(int64_t)c * taps + tap]));
   }
   st(y, (int64_t)t * ldy + c, dto, acc / (1.0f + expf(-acc)));
 }
@@ -357,20 +357,20 @@ __global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restri
 #pragma unroll
   for (int i = 0; i < VPL; ++i) s += v[i] * v[i];
   s = wave_sum(s);
-  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, inv_width), eps));
   TO* dst = y + (int64_t)row * ldy;
 #pragma unroll
   for (int i = 0; i < VPL / 4; ++i) {
     const int c = (i * 64 + lane) * 4;
     const float4_t ww = *reinterpret_cast<const float4_t*>(w + c);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[c + j] = static_cast<TO>(__fmul_rn(__fmul_rn(v[i * 4 + j], inverse), ww[j]));
+    for (int j = 0; j < 4; ++j) dst[c + j] = cvt_out<TO>(mul_rn(mul_rn(v[i * 4 + j], inverse), ww[j]));
   }
 }
 
 // Gated output norm for rows of 128: 16 lanes per row, 8 values per lane.
-template <class TZ, class TO>
-__global__ __launch_bounds__(256) void gated_rms128_kernel(const float* __restrict__ o, const TZ* __restrict__ z,
+template <class TOI, class TZ, class TO>
+__global__ __launch_bounds__(256) void gated_rms128_kernel(const TOI* __restrict__ o, const TZ* __restrict__ z,
                                                            int64_t ldz, const float* __restrict__ w,
                                                            TO* __restrict__ y, int T, int Hv, float eps) {
   const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -378,23 +378,31 @@ __global__ __launch_bounds__(256) void gated_rms128_kernel(const float* __restri
   if (row >= T * Hv) return;
   const int t = row / Hv, h = row % Hv;
   const int c = sub * 8;
-  const float* src = o + (int64_t)row * 128 + c;
-  const float4_t a = *reinterpret_cast<const float4_t*>(src);
-  const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
+  const TOI* src = o + (int64_t)row * 128 + c;
   const bool half_out = sizeof(TO) == 2;
   float v[8];
+  if constexpr (sizeof(TOI) == 2) {
+    const half8 oh = *reinterpret_cast<const half8*>(src);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(oh[j]);
+  } else {
+    const float4_t a = *reinterpret_cast<const float4_t*>(src);
+    const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
+  }
   if (half_out) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(static_cast<half_t>(v[j]));
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(to_f16(v[j]));
   }
+  // explicit fused steps: the compiler would otherwise contract some
+  // products into their sums, differently for f16 and f32 o
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) s += v[j] * v[j];
+  for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[j], v[j], s);
 #pragma unroll
   for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
-  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, 1.0f / 128.0f), eps));
+  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, 1.0f / 128.0f), eps));
   float zf[8];
   const TZ* zs = z + (int64_t)t * ldz + (int64_t)h * 128 + c;
   if (sizeof(TZ) == 2) {
@@ -408,9 +416,9 @@ __global__ __launch_bounds__(256) void gated_rms128_kernel(const float* __restri
   TO out[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    float n = __fmul_rn(__fmul_rn(v[j], inverse), w[c + j]);
-    if (half_out) n = static_cast<float>(static_cast<half_t>(n));
-    out[j] = static_cast<TO>(__fmul_rn(n, zf[j] / (1.0f + expf(-zf[j]))));
+    float n = mul_rn(mul_rn(v[j], inverse), w[c + j]);
+    if (half_out) n = static_cast<float>(to_f16(n));
+    out[j] = cvt_out<TO>(mul_rn(n, zf[j] / (1.0f + expf(-zf[j]))));
   }
   TO* dst = y + (int64_t)row * 128 + c;
 #pragma unroll
@@ -430,7 +438,7 @@ __global__ __launch_bounds__(256) void gates_kernel(const void* a, int64_t lda, 
 }
 
 // ---- gated output norm (qwen.rs:671-676): one wave per (token, head) row ----
-__global__ __launch_bounds__(256) void gated_rms_kernel(const float* o, const void* z, int64_t ldz,
+__global__ __launch_bounds__(256) void gated_rms_kernel(const void* o, int dto_in, const void* z, int64_t ldz,
                                                         int dtz, const float* w, void* y, int dto,
                                                         int T, int Hv, int width, float eps,
                                                         float inv_width) {
@@ -440,16 +448,16 @@ __global__ __launch_bounds__(256) void gated_rms_kernel(const float* o, const vo
   const int t = row / Hv, h = row % Hv;
   float s = 0.0f;
   for (int i = lane; i < width; i += 64) {
-    const float v = rnd(o[(int64_t)row * width + i], dto);
-    s += v * v;
+    const float v = rnd(ld(o, (int64_t)row * width + i, dto_in), dto);
+    s = __builtin_fmaf(v, v, s);
   }
   s = wave_sum(s);
-  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, inv_width), eps));
   for (int i = lane; i < width; i += 64) {
-    const float v = rnd(o[(int64_t)row * width + i], dto);
-    const float n = rnd(__fmul_rn(__fmul_rn(v, inverse), w[i]), dto);
+    const float v = rnd(ld(o, (int64_t)row * width + i, dto_in), dto);
+    const float n = rnd(mul_rn(mul_rn(v, inverse), w[i]), dto);
     const float zv = ld(z, (int64_t)t * ldz + (int64_t)h * width + i, dtz);
-    st(y, (int64_t)row * width + i, dto, __fmul_rn(n, zv / (1.0f + expf(-zv))));
+    st(y, (int64_t)row * width + i, dto, mul_rn(n, zv / (1.0f + expf(-zv))));
   }
 }
 
@@ -476,20 +484,20 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int6
     s += v * v;
   }
   s = wave_sum(s);
-  const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(s, inv_width), eps));
+  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, inv_width), eps));
   const int half = rot / 2;
   // position: pos0 + t, or pos0 + (t - first token of t's sequence)
   const float p = static_cast<float>(pos0 + (cu ? t - cu[seq_of(cu, nseq, t)] : t));
   const int64_t dst = ((int64_t)h * ldy_tok + dst_offset + t) * d;
   for (int i = lane; i < d; i += 64) {
-    const float v = rnd(__fmul_rn(__fmul_rn(ld(x, src + i, dti), inverse), w[i]), dto);
+    const float v = rnd(mul_rn(mul_rn(ld(x, src + i, dti), inverse), w[i]), dto);
     float out = v;
     if (i < rot) {
       const int j = i < half ? i + half : i - half;
-      const float vj = rnd(__fmul_rn(__fmul_rn(ld(x, src + j, dti), inverse), w[j]), dto);
+      const float vj = rnd(mul_rn(mul_rn(ld(x, src + j, dti), inverse), w[j]), dto);
       const float r = i < half ? -vj : vj;
-      const float ang = __fmul_rn(p, tab.inv_freq[i % half]);
-      out = __fadd_rn(__fmul_rn(v, cosf(ang)), __fmul_rn(r, sinf(ang)));
+      const float ang = mul_rn(p, tab.inv_freq[i % half]);
+      out = add_rn(mul_rn(v, cosf(ang)), mul_rn(r, sinf(ang)));
     }
     st(y, dst + i, dto, out);
   }
@@ -515,7 +523,7 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
   // position: pos0 + t, or pos0 + (t - first token of t's sequence)
   const float p = static_cast<float>(pos0 + (cu ? t - cu[seq_of(cu, nseq, t)] : t));
   for (int f = threadIdx.x; f < half; f += 256) {
-    const float ang = __fmul_rn(p, tab.inv_freq[f]);
+    const float ang = mul_rn(p, tab.inv_freq[f]);
     cs[f] = cosf(ang);
     sn[f] = sinf(ang);
   }
@@ -556,16 +564,16 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
 #pragma unroll
     for (int e = 0; e < EPL; ++e) ss += v[e] * v[e];
     ss = wave_sum(ss);
-    const float inverse = 1.0f / sqrtf(__fadd_rn(__fmul_rn(ss, inv_width), eps));
+    const float inverse = 1.0f / sqrtf(add_rn(mul_rn(ss, inv_width), eps));
 #pragma unroll
     for (int e = 0; e < EPL; ++e)
-      v[e] = static_cast<float>(static_cast<TO>(__fmul_rn(__fmul_rn(v[e], inverse), wv[e])));
+      v[e] = static_cast<float>(cvt_out<TO>(mul_rn(mul_rn(v[e], inverse), wv[e])));
     const int plane = i0 < half ? lane + pd : (i0 < rot ? lane - pd : lane);
     TO out[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       const float vj = __shfl(v[e], plane, 64);
-      out[e] = static_cast<TO>(i0 + e < rot ? __fadd_rn(__fmul_rn(v[e], cw[e]), __fmul_rn(vj, sw[e])) : v[e]);
+      out[e] = cvt_out<TO>(i0 + e < rot ? add_rn(mul_rn(v[e], cw[e]), mul_rn(vj, sw[e])) : v[e]);
     }
     TO* dst = y + ((int64_t)h * ldy_tok + dst_offset + t) * D + i0;
     bool done = false;
@@ -611,6 +619,32 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, int T, c
   const int t = static_cast<int>(idx / H), c = static_cast<int>(idx % H);
   const int id = min(max(ids[t], 0), vocab - 1);  // ids are validated by the caller
   h[idx] = ld(table, (int64_t)id * H + c, dt);
+}
+
+// 8 consecutive features per thread: one 16-byte (f16) or two 16-byte (f32)
+// row loads and two 16-byte stores
+template <class TT>
+__global__ __launch_bounds__(256) void embed_vec_kernel(const int32_t* __restrict__ ids, int T,
+                                                        const TT* __restrict__ table, int vocab, int H,
+                                                        float* __restrict__ h) {
+  const int per_row = H / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)T * per_row) return;
+  const int t = static_cast<int>(idx / per_row), c = static_cast<int>(idx % per_row) * 8;
+  const int id = min(max(ids[t], 0), vocab - 1);
+  const TT* src = table + (int64_t)id * H + c;
+  float4_t a, b;
+  if constexpr (sizeof(TT) == 2) {
+    const half8 v = *reinterpret_cast<const half8*>(src);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = static_cast<float>(v[j]), b[j] = static_cast<float>(v[4 + j]);
+  } else {
+    a = *reinterpret_cast<const float4_t*>(src);
+    b = *reinterpret_cast<const float4_t*>(src + 4);
+  }
+  float* dst = h + (int64_t)t * H + c;
+  *reinterpret_cast<float4_t*>(dst) = a;
+  *reinterpret_cast<float4_t*>(dst + 4) = b;
 }
 
 __global__ __launch_bounds__(64) void head_kernel(const float* x, int H, const float* w, float* logits) {
@@ -769,34 +803,40 @@ extern "C" int clef_delta_gates(const void* a, int64_t lda, const void* b, int64
   return check_launch("delta_gates");
 }
 
-extern "C" int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, int dtype_z,
+extern "C" int clef_gated_rms_silu(const void* o, int dtype_o, const void* z, int64_t ldz, int dtype_z,
                                    const float* w, void* y, int dtype_out, int T, int Hv, int width,
                                    float eps, void* stream) {
   if (ldz == 0) ldz = (int64_t)Hv * width;
   CLEF_REQUIRE(o && z && w && y, "gated norm: null pointer");
   CLEF_REQUIRE(T >= 1 && Hv >= 1 && width >= 1 && ldz >= (int64_t)Hv * width, "gated norm: dimensions");
-  CLEF_REQUIRE(dtype_ok(dtype_z) && dtype_ok(dtype_out), "gated norm: dtype");
+  CLEF_REQUIRE(dtype_ok(dtype_o) && dtype_ok(dtype_z) && dtype_ok(dtype_out), "gated norm: dtype");
+  hipStream_t st = static_cast<hipStream_t>(stream);
   if (width == 128 && ldz % 8 == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
     const dim3 g((T * Hv + 15) / 16);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (dtype_z == CLEF_F16 && dtype_out == CLEF_F16)
-      hipLaunchKernelGGL((gated_rms128_kernel<half_t, half_t>), g, dim3(256), 0, st, o,
-                         static_cast<const half_t*>(z), ldz, w, static_cast<half_t*>(y), T, Hv, eps);
-    else if (dtype_z == CLEF_F16)
-      hipLaunchKernelGGL((gated_rms128_kernel<half_t, float>), g, dim3(256), 0, st, o,
-                         static_cast<const half_t*>(z), ldz, w, static_cast<float*>(y), T, Hv, eps);
-    else if (dtype_out == CLEF_F16)
-      hipLaunchKernelGGL((gated_rms128_kernel<float, half_t>), g, dim3(256), 0, st, o,
-                         static_cast<const float*>(z), ldz, w, static_cast<half_t*>(y), T, Hv, eps);
-    else
-      hipLaunchKernelGGL((gated_rms128_kernel<float, float>), g, dim3(256), 0, st, o,
-                         static_cast<const float*>(z), ldz, w, static_cast<float*>(y), T, Hv, eps);
+#define CLEF_GRMS(TOI, TZ, TO)                                                                                   \
+  hipLaunchKernelGGL((gated_rms128_kernel<TOI, TZ, TO>), g, dim3(256), 0, st, static_cast<const TOI*>(o),      \
+                     static_cast<const TZ*>(z), ldz, w, static_cast<TO*>(y), T, Hv, eps)
+#define CLEF_GRMS_O(TZ, TO)        \
+  if (dtype_o == CLEF_F16)         \
+    CLEF_GRMS(half_t, TZ, TO);     \
+  else                             \
+    CLEF_GRMS(float, TZ, TO)
+    if (dtype_z == CLEF_F16 && dtype_out == CLEF_F16) {
+      CLEF_GRMS_O(half_t, half_t);
+    } else if (dtype_z == CLEF_F16) {
+      CLEF_GRMS_O(half_t, float);
+    } else if (dtype_out == CLEF_F16) {
+      CLEF_GRMS_O(float, half_t);
+    } else {
+      CLEF_GRMS_O(float, float);
+    }
+#undef CLEF_GRMS_O
+#undef CLEF_GRMS
     return check_launch("gated_rms_silu");
   }
-  hipLaunchKernelGGL(gated_rms_kernel, dim3((T * Hv + 3) / 4), dim3(256), 0, (hipStream_t)stream, o,
-                     z, ldz, dtype_z, w, y, dtype_out, T, Hv, width, eps,
-                     static_cast<float>(1.0 / static_cast<double>(width)));
+  hipLaunchKernelGGL(gated_rms_kernel, dim3((T * Hv + 3) / 4), dim3(256), 0, st, o, dtype_o, z, ldz, dtype_z, w,
+                     y, dtype_out, T, Hv, width, eps, static_cast<float>(1.0 / static_cast<double>(width)));
   return check_launch("gated_rms_silu");
 }
 
@@ -907,9 +947,21 @@ extern "C" int clef_embed(const int32_t* ids, int T, const void* table, int dtyp
                           float* h, void* stream) {
   CLEF_REQUIRE(ids && table && h, "embed: null pointer");
   CLEF_REQUIRE(T >= 1 && vocab >= 1 && H >= 1 && dtype_ok(dtype), "embed: dimensions");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (H % 8 == 0 && ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(h)) & 15) == 0) {
+    const int64_t n = (int64_t)T * (H / 8);
+    const dim3 g((unsigned)((n + 255) / 256));
+    if (dtype == CLEF_F16)
+      hipLaunchKernelGGL(embed_vec_kernel<half_t>, g, dim3(256), 0, st, ids, T, static_cast<const half_t*>(table),
+                         vocab, H, h);
+    else
+      hipLaunchKernelGGL(embed_vec_kernel<float>, g, dim3(256), 0, st, ids, T, static_cast<const float*>(table),
+                         vocab, H, h);
+    return check_launch("embed");
+  }
   const int64_t n = (int64_t)T * H;
-  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     ids, T, table, dtype, vocab, H, h);
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, ids, T, table, dtype,
+                     vocab, H, h);
   return check_launch("embed");
 }
 

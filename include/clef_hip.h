@@ -193,13 +193,13 @@ int clef_delta_gates_proj(const void* x, int64_t ldx, const void* packed, int K,
  * Gated output norm, qwen.rs:671-676: per token and v-head row of `width`,
  * o is rounded to dtype_out (the scan output cast to the activation dtype),
  * RMS-normalised in f32 with w (no offset), rounded to dtype_out, multiplied
- * by silu(z) in f32 and rounded to dtype_out.  o: [T, Hv, width] f32
- * contiguous; z: [T, Hv, width] with token stride ldz (dtype_z); y: [T,
- * Hv*width] contiguous.
+ * by silu(z) in f32 and rounded to dtype_out.  o: [T, Hv, width] contiguous
+ * in dtype_o (a scan that already wrote o in f16 gives the same values as
+ * rounding its f32 output here); z: [T, Hv, width] with token stride ldz
+ * (dtype_z); y: [T, Hv*width] contiguous.
  */
-int clef_gated_rms_silu(const float* o, const void* z, int64_t ldz, int dtype_z, const float* w,
-                        void* y, int dtype_out, int T, int Hv, int width, float eps,
-                        void* stream);
+int clef_gated_rms_silu(const void* o, int dtype_o, const void* z, int64_t ldz, int dtype_z, const float* w,
+                        void* y, int dtype_out, int T, int Hv, int width, float eps, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Gated full-attention layer pieces (qwen.rs:451-525; ops.rs:62-188)      */

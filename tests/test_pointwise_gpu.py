@@ -64,6 +64,19 @@ def test_rms_matches_oracle(clef, rows, width, dt_out):
 
 
 @gpu
+@pytest.mark.parametrize("T,Hv,width", [(300, 32, 128), (7, 3, 64)])
+def test_gated_rms_silu_reads_rounded_scan_output(clef, T, Hv, width):
+    """An f16 scan output gives exactly what rounding the f32 one inside the
+    norm gives (the mixed block feeds the norm f16 o)."""
+    gen = torch.Generator(device="cuda").manual_seed(T + 1)
+    o = torch.randn((T, Hv, width), generator=gen, device="cuda")
+    z = torch.randn((T, Hv * width), generator=gen, device="cuda").half()
+    w = torch.randn((width,), generator=gen, device="cuda")
+    assert torch.equal(clef.gated_rms_silu(o, z, w, out_dtype=torch.float16),
+                       clef.gated_rms_silu(o.half(), z, w, out_dtype=torch.float16))
+
+
+@gpu
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
 @pytest.mark.parametrize("T,Hv,width", [(300, 32, 128), (20, 2, 4), (7, 3, 64)])
 def test_gated_rms_silu(clef, dt, T, Hv, width):
