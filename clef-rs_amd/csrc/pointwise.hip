@@ -363,66 +363,108 @@ __global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restri
   for (int i = 0; i < VPL / 4; ++i) {
     const int c = (i * 64 + lane) * 4;
     const float4_t ww = *reinterpret_cast<const float4_t*>(w + c);
+    float4_t o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[c + j] = cvt_out<TO>(mul_rn(mul_rn(v[i * 4 + j], inverse), ww[j]));
+    for (int j = 0; j < 4; ++j) o[j] = mul_rn(mul_rn(v[i * 4 + j], inverse), ww[j]);
+    if constexpr (sizeof(TO) == 2) {  // one 8-byte store of the four rounded values
+      half4 h;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = to_f16(o[j]);
+      *reinterpret_cast<half4*>(dst + c) = h;
+    } else {
+      *reinterpret_cast<float4_t*>(dst + c) = o;
+    }
   }
 }
 
-// Gated output norm for rows of 128: 16 lanes per row, 8 values per lane.
-template <class TOI, class TZ, class TO>
-__global__ __launch_bounds__(256) void gated_rms128_kernel(const TOI* __restrict__ o, const TZ* __restrict__ z,
-                                                           int64_t ldz, const float* __restrict__ w,
-                                                           TO* __restrict__ y, int T, int Hv, float eps) {
-  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  if (row >= T * Hv) return;
-  const int t = row / Hv, h = row % Hv;
-  const int c = sub * 8;
-  const TOI* src = o + (int64_t)row * 128 + c;
-  const bool half_out = sizeof(TO) == 2;
-  float v[8];
-  if constexpr (sizeof(TOI) == 2) {
-    const half8 oh = *reinterpret_cast<const half8*>(src);
+// Gated output norm for rows of 128: 16 lanes per row, 8 values per lane,
+// kGatedRows rows per 16-lane group (rows g, g + 16, ... of the work-group's
+// block; their o and z loads are requested before the first row is reduced).
+// The kernel is bound by vector ALU work rather than bytes (16.8M elements
+// per DeltaNet layer at T = 4096), so SiLU uses the hardware exp2 and
+// reciprocal (silu_hw) instead of expf and an IEEE division.
+constexpr int kGatedRows = 1;
+
+// Sum over each row of 16 lanes with DPP moves (no LDS round trips): lane
+// partners xor 1 and xor 2 (quad permutes), then the half-row and row
+// mirrors, which pair the same quads and halves as xor 4 and xor 8.  Each
+// step adds a value to its partner's, so every lane of a row ends with the
+// same bits, summed in the association of an xor butterfly.
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_partner<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_partner<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_partner<0x141>(v);  // row_half_mirror
+  v += dpp_partner<0x140>(v);  // row_mirror
+  return v;
+}
+
+template <class T8>
+__device__ __forceinline__ void load8_f32(const T8* src, float* v) {
+  if constexpr (sizeof(T8) == 2) {
+    const half8 h = *reinterpret_cast<const half8*>(src);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(oh[j]);
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(h[j]);
   } else {
     const float4_t a = *reinterpret_cast<const float4_t*>(src);
     const float4_t b = *reinterpret_cast<const float4_t*>(src + 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = a[j], v[4 + j] = b[j];
   }
-  if (half_out) {
+}
+
+template <class TOI, class TZ, class TO>
+__global__ __launch_bounds__(256) void gated_rms128_kernel(const TOI* __restrict__ o, const TZ* __restrict__ z,
+                                                           int64_t ldz, const float* __restrict__ w,
+                                                           TO* __restrict__ y, int T, int Hv, float eps) {
+  const int rows = T * Hv;
+  const int row0 = blockIdx.x * (16 * kGatedRows) + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const int c = sub * 8;
+  const bool half_out = sizeof(TO) == 2;
+  // a 16-lane group shares its row, so a group is active or inactive as a
+  // whole and the shuffles below stay inside active groups
+  float v[kGatedRows][8], zf[kGatedRows][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(to_f16(v[j]));
+  for (int k = 0; k < kGatedRows; ++k) {
+    const int row = row0 + 16 * k;
+    if (row < rows) {
+      const int t = row / Hv, h = row % Hv;
+      load8_f32(o + (int64_t)row * 128 + c, v[k]);
+      load8_f32(z + (int64_t)t * ldz + (int64_t)h * 128 + c, zf[k]);
+    }
   }
-  // explicit fused steps: the compiler would otherwise contract some
-  // products into their sums, differently for f16 and f32 o
-  float s = 0.0f;
+  float wv[8];
+  load8_f32(w + c, wv);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[j], v[j], s);
+  for (int k = 0; k < kGatedRows; ++k) {
+    const int row = row0 + 16 * k;
+    if (row >= rows) break;
+    if (half_out) {
 #pragma unroll
-  for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
-  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, 1.0f / 128.0f), eps));
-  float zf[8];
-  const TZ* zs = z + (int64_t)t * ldz + (int64_t)h * 128 + c;
-  if (sizeof(TZ) == 2) {
-    const half8 zh = *reinterpret_cast<const half8*>(zs);
+      for (int j = 0; j < 8; ++j) v[k][j] = static_cast<float>(to_f16(v[k][j]));
+    }
+    // explicit fused steps: the compiler would otherwise contract some
+    // products into their sums, differently for f16 and f32 o
+    float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) zf[j] = static_cast<float>(zh[j]);
-  } else {
+    for (int j = 0; j < 8; ++j) s = __builtin_fmaf(v[k][j], v[k][j], s);
+    s = sum16(s);
+    const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, 1.0f / 128.0f), eps));
+    TO out[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) zf[j] = static_cast<float>(zs[j]);
+    for (int j = 0; j < 8; ++j) {
+      float n = mul_rn(mul_rn(v[k][j], inverse), wv[j]);
+      if (half_out) n = static_cast<float>(to_f16(n));
+      out[j] = cvt_out<TO>(mul_rn(n, silu_hw(zf[k][j])));
+    }
+    TO* dst = y + (int64_t)row * 128 + c;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dst[j] = out[j];
   }
-  TO out[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float n = mul_rn(mul_rn(v[j], inverse), w[c + j]);
-    if (half_out) n = static_cast<float>(to_f16(n));
-    out[j] = cvt_out<TO>(mul_rn(n, zf[j] / (1.0f + expf(-zf[j]))));
-  }
-  TO* dst = y + (int64_t)row * 128 + c;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) dst[j] = out[j];
 }
 
 // ---- decay and write strength (qwen.rs:619-627) -----------------------------
@@ -457,7 +499,7 @@ __global__ __launch_bounds__(256) void gated_rms_kernel(const void* o, int dto_i
     const float v = rnd(ld(o, (int64_t)row * width + i, dto_in), dto);
     const float n = rnd(mul_rn(mul_rn(v, inverse), w[i]), dto);
     const float zv = ld(z, (int64_t)t * ldz + (int64_t)h * width + i, dtz);
-    st(y, (int64_t)row * width + i, dto, mul_rn(n, zv / (1.0f + expf(-zv))));
+    st(y, (int64_t)row * width + i, dto, mul_rn(n, silu_hw(zv)));
   }
 }
 
@@ -672,8 +714,10 @@ extern "C" int clef_rms_norm(const void* x, int64_t ldx, int dtype_in, const flo
   CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "RMS: dtype");
   CLEF_REQUIRE(eps > 0.0f && eps <= 1.0f, "RMS: epsilon");
   const float inv_w = static_cast<float>(1.0 / static_cast<double>(width));
-  const bool vec = dtype_in == CLEF_F32 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+  // (4-element vector loads of x and w, 4-element stores of y)
+  const bool vec = dtype_in == CLEF_F32 && ldx % 4 == 0 && ldy % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                     reinterpret_cast<uintptr_t>(y)) & 15) == 0;
   if (vec && (width == 2048 || width == 1024)) {
     const dim3 g((rows + 3) / 4);
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -811,9 +855,9 @@ extern "C" int clef_gated_rms_silu(const void* o, int dtype_o, const void* z, in
   CLEF_REQUIRE(T >= 1 && Hv >= 1 && width >= 1 && ldz >= (int64_t)Hv * width, "gated norm: dimensions");
   CLEF_REQUIRE(dtype_ok(dtype_o) && dtype_ok(dtype_z) && dtype_ok(dtype_out), "gated norm: dtype");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (width == 128 && ldz % 8 == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
-    const dim3 g((T * Hv + 15) / 16);
+  if (width == 128 && ldz % 8 == 0 &&
+      ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(w)) & 15) == 0) {
+    const dim3 g((T * Hv + 16 * kGatedRows - 1) / (16 * kGatedRows));
 #define CLEF_GRMS(TOI, TZ, TO)                                                                                   \
   hipLaunchKernelGGL((gated_rms128_kernel<TOI, TZ, TO>), g, dim3(256), 0, st, static_cast<const TOI*>(o),      \
                      static_cast<const TZ*>(z), ldz, w, static_cast<TO*>(y), T, Hv, eps)
