@@ -92,11 +92,6 @@ struct Row8<float> {
   __device__ __forceinline__ float at(int j) const { return j < 4 ? a[j] : b[j - 4]; }
 };
 
-// SiLU with the hardware exp2 and reciprocal: x / (1 + e^-x) to a relative
-// error of about 1e-6 (the argument's rounding, |x| log2(e) ulp, dominates).
-__device__ __forceinline__ float silu_hw(float x) {
-  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
-}
 
 // Vectorised conv + SiLU: 8 consecutive channels per thread and a run of
 // kConvRun tokens (taps <= 4; T4: taps == 4 known at compile time).  The
