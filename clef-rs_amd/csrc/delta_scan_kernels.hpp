@@ -215,10 +215,114 @@ __device__ __forceinline__ void chunk_at(const ScanParams& p, int c, int& t0, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Conv prologue (ScanParams::mixed): the mixer's causal conv + SiLU computed
+// where its outputs are consumed, in the separate conv kernel's order and
+// roundings (taps oldest -> newest, each product and sum rounded, hardware
+// SiLU, the result rounded to the input dtype), so the scan sees the same q,
+// k and v values.
+
+// Sequence of token t and its first token (one sequence: 0 and 0).
+__device__ __forceinline__ void conv_sequence(const ScanParams& p, int t, int& seq, int& start) {
+  seq = 0;
+  start = 0;
+  if (!p.cu_seqlens) return;
+  int lo = 0, hi = p.nseq - 1;  // the last s with cu_seqlens[s] <= t
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.cu_seqlens[mid] <= t)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  seq = lo;
+  start = p.cu_seqlens[lo];
+}
+
+// Channels ch .. ch+VI-1 of token tp: a row of `mixed` (clamped to `last`,
+// the chunk's last token) from the sequence start on, before it the
+// sequence's history rows, before those zero (a zero product added to the
+// running sum leaves it unchanged, as skipping the tap does).
+template <class IT>
+__device__ __forceinline__ void conv_load(const ScanParams& p, int tp, int last, int seq, int start, int ch,
+                                          float* x) {
+  constexpr int VI = Vec16<IT>::n;
+  if (tp >= start) {
+    const IT* row = static_cast<const IT*>(p.mixed) + (int64_t)min(tp, last) * p.ld_mixed + ch;
+    const typename Vec16<IT>::type v = *reinterpret_cast<const typename Vec16<IT>::type*>(row);
+#pragma unroll
+    for (int i = 0; i < VI; ++i) x[i] = static_cast<float>(v[i]);
+    return;
+  }
+  const int hr = p.hist_rows + (tp - start);
+  if (p.conv_hist && hr >= 0) {
+    const float* h = p.conv_hist + (int64_t)seq * p.hist_stride + (int64_t)hr * p.conv_channels + ch;
+#pragma unroll
+    for (int i = 0; i < VI; ++i) x[i] = h[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < VI; ++i) x[i] = 0.0f;
+  }
+}
+
+// RPT consecutive rows (chunk rows r0 .. r0+RPT-1) of VI channels from ch:
+// y[j][i] = round_IT(silu(sum_tap x[t-3+tap] w[tap])); rows past the chunk's
+// n tokens and inactive lanes give 0.
+template <class IT, int RPT>
+__device__ __forceinline__ void conv_rows(const ScanParams& p, int t0, int n, int r0, int seq, int start, int ch,
+                                          bool active, float (*y)[Vec16<IT>::n]) {
+  constexpr int VI = Vec16<IT>::n;
+  float w[VI][4];
+  float xr[RPT + 3][VI];
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const float4_t w4 = *reinterpret_cast<const float4_t*>(p.conv_w + (int64_t)(ch + i) * 4);
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) w[i][tap] = w4[tap];
+    }
+#pragma unroll
+    for (int k = 0; k < RPT + 3; ++k) conv_load<IT>(p, t0 + r0 + k - 3, t0 + n - 1, seq, start, ch, xr[k]);
+  }
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap) acc = add_rn(acc, mul_rn(xr[j + tap][i], w[i][tap]));
+      const float v = silu_hw(acc);
+      y[j][i] = (active && r0 + j < n) ? (sizeof(IT) == 2 ? static_cast<float>(to_f16(v)) : v) : 0.0f;
+    }
+  }
+}
+
+// l2 normalisation of one row held by TPR consecutive lanes (VI values each),
+// eps inside the sqrt (qwen.rs:837-840), times the query scale for q; the
+// explicit fmaf steps fix the association for every caller.
+template <class CT, int VI, int TPR>
+__device__ __forceinline__ void l2norm_row(const float* x, float extra, CT* dst) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VI; ++i) s = fmaf(x[i], x[i], s);
+#pragma unroll
+  for (int off = 1; off < TPR; off <<= 1) s += __shfl_xor(s, off, 64);
+  const float inv = 1.0f / sqrtf(s + 1e-6f);
+  const float scale = inv * extra;
+#pragma unroll
+  for (int i = 0; i < VI; ++i) {
+    const float v = x[i] * scale;
+    if constexpr (sizeof(CT) == 2)
+      dst[i] = to_f16(v);
+    else
+      dst[i] = v;
+  }
+}
+
 // Kernel 1: per (chunk, k-head) preparation of every state-independent
 // operand of the chunk, for all v-heads of the k-head.
 // ---------------------------------------------------------------------------
-template <class CT, class IT, int DK>
+template <class CT, class IT, int DK, bool CONV>
 __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   typedef Geo<CT, DK> G;
   constexpr int EPF = G::EPF, KB = G::KB, TPK = G::TPK, NKX = G::NKX, NKT = G::NKT, NST = G::NST;
@@ -260,44 +364,53 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   const int cap_row = p.capture > 0 ? (p.capture - 1) % kC : 0;
 
   // ---- 1. loads: q/k rows (clamped), g and beta of the first v-head
-  const IT* qbase = static_cast<const IT*>(p.q);
-  const IT* kbase = static_cast<const IT*>(p.k);
-  typename Vec16<IT>::type raw[NPASS];
-#pragma unroll
-  for (int ps = 0; ps < NPASS; ++ps) {
-    const int rr = ps * RPP + tid / TPR;
-    const bool isq = rr >= kC;
-    const int r = isq ? rr - kC : rr;
-    const IT* row = (isq ? qbase : kbase) + (int64_t)(t0 + min(r, n - 1)) * p.sqk + (int64_t)hk * dk;
-    raw[ps] = load_row_raw<IT>(row, (tid % TPR) * VI, dk, p.vec_qk);
-  }
   uint32_t gbits = 0, bbits = 0;
   if (wave == 0) {
     const int64_t gi = (int64_t)(t0 + min(lane, n - 1)) * p.sgb + (int64_t)hk * rep;
     gbits = load_bits(p.g, gi, p.dtype_gb);
     bbits = load_bits(p.beta, gi, p.dtype_gb);
   }
-  // l2-normalise rows into LDS (eps inside the sqrt, qwen.rs:837-840); zero
-  // padding rows and columns dk..DK-1
+  if constexpr (CONV) {
+    // the conv prologue: lane group g (TPR lanes) holds chunk rows
+    // RPT g .. RPT g + RPT - 1 of k, then of q, VI channels per lane
+    constexpr int RPT = TPR / 4;
+    const int g = tid / TPR, e0 = (tid % TPR) * VI;
+    int seq, start;
+    conv_sequence(p, t0, seq, start);
 #pragma unroll
-  for (int ps = 0; ps < NPASS; ++ps) {
-    const int rr = ps * RPP + tid / TPR;
-    const bool isq = rr >= kC;
-    const int r = isq ? rr - kC : rr;
-    const int e0 = (tid % TPR) * VI;
-    float x[VI];
+    for (int m = 0; m < 2; ++m) {
+      const bool isq = m == 1;
+      const int ch = (isq ? 0 : p.Hk * dk) + hk * dk + e0;  // [q | k | v] channels
+      float y[RPT][VI];
+      conv_rows<IT, RPT>(p, t0, n, RPT * g, seq, start, ch, e0 < dk, y);
 #pragma unroll
-    for (int i = 0; i < VI; ++i) x[i] = (r < n && e0 + i < dk) ? static_cast<float>(raw[ps][i]) : 0.0f;
-    float s = 0.0f;
+      for (int j = 0; j < RPT; ++j)
+        l2norm_row<CT, VI, TPR>(y[j], isq ? p.qscale : 1.0f, (isq ? sQ : sK) + (RPT * g + j) * LDR + e0);
+    }
+  } else {
+    const IT* qbase = static_cast<const IT*>(p.q);
+    const IT* kbase = static_cast<const IT*>(p.k);
+    typename Vec16<IT>::type raw[NPASS];
 #pragma unroll
-    for (int i = 0; i < VI; ++i) s += x[i] * x[i];
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int rr = ps * RPP + tid / TPR;
+      const bool isq = rr >= kC;
+      const int r = isq ? rr - kC : rr;
+      const IT* row = (isq ? qbase : kbase) + (int64_t)(t0 + min(r, n - 1)) * p.sqk + (int64_t)hk * dk;
+      raw[ps] = load_row_raw<IT>(row, (tid % TPR) * VI, dk, p.vec_qk);
+    }
+    // l2-normalise rows into LDS; zero padding rows and columns dk..DK-1
 #pragma unroll
-    for (int off = 1; off < TPR; off <<= 1) s += __shfl_xor(s, off, 64);
-    const float inv = 1.0f / sqrtf(s + 1e-6f);
-    const float scale = isq ? inv * p.qscale : inv;
-    CT* dst = (isq ? sQ : sK) + r * LDR + e0;
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int rr = ps * RPP + tid / TPR;
+      const bool isq = rr >= kC;
+      const int r = isq ? rr - kC : rr;
+      const int e0 = (tid % TPR) * VI;
+      float x[VI];
 #pragma unroll
-    for (int i = 0; i < VI; ++i) dst[i] = static_cast<CT>(x[i] * scale);
+      for (int i = 0; i < VI; ++i) x[i] = (r < n && e0 + i < dk) ? static_cast<float>(raw[ps][i]) : 0.0f;
+      l2norm_row<CT, VI, TPR>(x, isq ? p.qscale : 1.0f, (isq ? sQ : sK) + r * LDR + e0);
+    }
   }
   lds_barrier();
 
@@ -503,6 +616,32 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       }
     }
     lds_barrier();  // before the next v-head rewrites sA, sTT, sM, sGam
+  }
+
+  if constexpr (CONV) {
+    // ---- 4. the convolved v of this k-head's v-heads, for the carry
+    // (rows of this chunk only; p.v has token stride p.sv, dv == dk)
+    constexpr int RPT = TPR / 4;
+    const int g = tid / TPR, e0 = (tid % TPR) * VI;
+    int seq, start;
+    conv_sequence(p, t0, seq, start);
+    IT* vout = static_cast<IT*>(const_cast<void*>(p.v));
+    for (int v = 0; v < rep; ++v) {
+      const int h = hk * rep + v;
+      const int ch = 2 * p.Hk * dk + h * p.dv + e0;
+      float y[RPT][VI];
+      conv_rows<IT, RPT>(p, t0, n, RPT * g, seq, start, ch, e0 < p.dv, y);
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int r = RPT * g + j;
+        if (r < n && e0 < p.dv) {
+          typename Vec16<IT>::type o;
+#pragma unroll
+          for (int i = 0; i < VI; ++i) o[i] = static_cast<IT>(y[j][i]);  // exact: y holds IT values
+          *reinterpret_cast<typename Vec16<IT>::type*>(vout + (int64_t)(t0 + r) * p.sv + (int64_t)h * p.dv + e0) = o;
+        }
+      }
+    }
   }
 }
 
@@ -1028,7 +1167,10 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
 
 template <class CT, class IT, int DK>
 int launch_dk(const ScanParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((scan_prepare<CT, IT, DK>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
+  if (p.mixed)
+    hipLaunchKernelGGL((scan_prepare<CT, IT, DK, true>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((scan_prepare<CT, IT, DK, false>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
   int rc = check_launch("scan_prepare");
   if (rc) return rc;
   const int ntiles = (p.dv + kVT - 1) / kVT;

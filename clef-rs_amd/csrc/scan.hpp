@@ -40,6 +40,20 @@ struct ScanParams {
   int* nchunk_total;      // valid entries of chunk_tab
   int nseq;
   int64_t init_stride;    // floats between consecutive sequences' initial states (0: shared)
+  // Conv prologue (qwen.rs:609-618, 765-796, 4 taps): when `mixed` is set, q,
+  // k and v are the raw projection columns [q | k | v] of `mixed` (token
+  // stride ld_mixed, dtype_qkv); scan_prepare applies the causal conv + SiLU
+  // (rounded to dtype_qkv, as the separate conv kernel stores it), and writes
+  // the convolved v to `v` (token stride sv) for the carry.  Rows before a
+  // sequence's first token come from its f32 history (hist_rows rows of
+  // conv_channels, sequence s at conv_hist + s * hist_stride), else zero.
+  const void* mixed;
+  int64_t ld_mixed;
+  const float* conv_w;     // [conv_channels][4]
+  const float* conv_hist;
+  int hist_rows;
+  int64_t hist_stride;
+  int conv_channels;       // 2 Hk dk + Hv dv
 };
 
 // nseq > 1 (or a cu_seqlens table) sizes for a ragged batch of T tokens

@@ -1,0 +1,92 @@
+"""The mixer's conv + SiLU folded into the scan (clef_delta_scan_conv; the
+projection -> causal conv -> SiLU -> recurrence steps of qwen.rs:603-618,
+765-796, 826-882): the same output, final and captured states and convolved
+v as the separate conv kernel (clef_conv_silu / clef_conv_silu_varlen)
+followed by the scan, bit for bit, with and without history rows, over one
+sequence and a ragged batch."""
+import numpy as np
+import pytest
+import torch
+
+gpu = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def clef():
+    import clef_hip
+    clef_hip.lib()
+    return clef_hip
+
+
+def _inputs(seed, T, Hk, Hv, d, dtype):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    W = 2 * Hk * d + Hv * d
+    mixed = torch.randn((T, W + 64), generator=gen, device="cuda").to(dtype)  # + 64 columns as z would be
+    conv_w = 0.5 * torch.randn((W, 4), generator=gen, device="cuda")
+    g = -torch.nn.functional.softplus(torch.randn((T, Hv), generator=gen, device="cuda"))
+    beta = torch.sigmoid(torch.randn((T, Hv), generator=gen, device="cuda"))
+    hist = torch.randn((3, W), generator=gen, device="cuda")
+    return mixed, conv_w, g, beta, hist, W
+
+
+def _split(y, T, Hk, Hv, d):
+    q = y[:, :Hk * d].view(T, Hk, d)
+    k = y[:, Hk * d:2 * Hk * d].view(T, Hk, d)
+    v = y[:, 2 * Hk * d:].view(T, Hv, d)
+    return q, k, v
+
+
+@gpu
+@pytest.mark.parametrize("precision", ["strict", "mixed"])
+@pytest.mark.parametrize("T,Hk,Hv,d,hist_rows,capture", [(300, 2, 4, 64, 0, 0), (200, 2, 4, 64, 3, 77),
+                                                         (65, 1, 2, 32, 2, 65), (4096, 16, 32, 128, 0, 0)])
+def test_fused_conv_scan_equals_conv_then_scan(clef, precision, T, Hk, Hv, d, hist_rows, capture):
+    dt = torch.float32 if precision == "strict" else torch.float16
+    mixed, conv_w, g, beta, hist, W = _inputs(T + d, T, Hk, Hv, d, dt)
+    history = hist[3 - hist_rows:].contiguous() if hist_rows else None
+    init = 0.1 * torch.randn((Hv, d, d), generator=torch.Generator(device="cuda").manual_seed(1), device="cuda")
+    scan = clef.DeltaScan(d, d, precision)
+    y = clef.conv_silu(mixed[:, :W], conv_w, history=history, out_dtype=dt)
+    q, k, v = _split(y, T, Hk, Hv, d)
+    out_ref, cap_ref, fin_ref = scan.prefill(q, k, v, g, beta, initial=init, capture=capture)
+    out, vconv, cap, fin = clef.delta_scan_conv(scan, mixed, Hk, Hv, conv_w, g, beta, history=history,
+                                                initial=init, capture=capture)
+    assert torch.equal(vconv, v)
+    assert torch.equal(out, out_ref)
+    assert torch.equal(fin, fin_ref)
+    if capture:
+        assert torch.equal(cap, cap_ref)
+
+
+@gpu
+@pytest.mark.parametrize("precision", ["strict", "mixed"])
+@pytest.mark.parametrize("with_history", [False, True])
+def test_fused_conv_scan_ragged_batch(clef, precision, with_history):
+    """Sequences of 0, 1, 63, 64, 65 tokens cover the partial-chunk and
+    sequence-start edges; the history (a shared prefix's conv rows) feeds
+    every sequence's first three tokens."""
+    lens = [200, 0, 1, 63, 64, 65, 130, 7]
+    Hk, Hv, d = 2, 4, 64
+    T = sum(lens)
+    dt = torch.float32 if precision == "strict" else torch.float16
+    mixed, conv_w, g, beta, hist, W = _inputs(11, T, Hk, Hv, d, dt)
+    history = hist if with_history else None
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
+    init = 0.1 * torch.randn((Hv, d, d), generator=torch.Generator(device="cuda").manual_seed(2), device="cuda")
+    scan = clef.DeltaScan(d, d, precision)
+    y = clef.conv_silu_varlen(mixed[:, :W], conv_w, cu, history=history, out_dtype=dt)
+    q, k, v = _split(y, T, Hk, Hv, d)
+    out_ref, fin_ref = scan.prefill_varlen(q, k, v, g, beta, cu, initial=init)
+    out, vconv, _, fin = clef.delta_scan_conv(scan, mixed, Hk, Hv, conv_w, g, beta, history=history,
+                                              cu_seqlens=cu, initial=init)
+    assert torch.equal(vconv, v)
+    assert torch.equal(out, out_ref)
+    assert torch.equal(fin, fin_ref)
+
+
+def test_fused_conv_scan_rejects_other_tap_counts(clef):
+    """Validation happens before any launch (no GPU needed)."""
+    rc = clef.lib().clef_delta_scan_conv(
+        None, 0, 1, None, 3, None, 0, 0, None, None, None, 0, 0, None, 1, 64, 1, 1, 64, 64, 64, 1,
+        None, 0, 0, None, 0, 0, None, None, None, 0, None)
+    assert rc < 0
