@@ -209,6 +209,11 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(gemm_tfs / MFMA_PEAK_TFS[dt], 4),
             "traffic": measured_traffic(T, args.profile),
+            # per launch (event-timed on the backbone's stream), to set beside
+            # the kernel-trace averages
+            "launches_per_step": int(g["launches"]),
+            "avg_launch_us": round(g["ms"] * 1e3 / g["launches"], 2),
+            "flops_per_launch": g["flops"] / g["launches"],
         },
         "scan": {
             "in_block_GBs": round(scan_gbs, 1),

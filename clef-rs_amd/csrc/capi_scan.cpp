@@ -157,6 +157,12 @@ extern "C" int clef_delta_scan_conv(const void* mixed, int64_t ld_mixed, int dty
   CLEF_REQUIRE(history_rows >= 0 && history_rows <= taps - 1 && history_stride >= 0,
                "DeltaNet scan (conv): history rows in 0..3, stride >= 0");
   CLEF_REQUIRE(initial_stride >= 0, "DeltaNet scan (conv): negative initial-state stride");
+  {  // the prepare reads mixed while it writes v_conv
+    const size_t e = dtype_qkv == CLEF_F32 ? 4 : 2;
+    const uintptr_t m0 = reinterpret_cast<uintptr_t>(mixed), m1 = m0 + e * static_cast<size_t>(T) * ld_mixed;
+    const uintptr_t v0 = reinterpret_cast<uintptr_t>(v_conv), v1 = v0 + e * static_cast<size_t>(T) * Hv * dv;
+    CLEF_REQUIRE(v1 <= m0 || m1 <= v0, "DeltaNet scan (conv): v_conv overlaps mixed");
+  }
   const bool ragged = cu_seqlens != nullptr;
   if (ragged) {
     CLEF_REQUIRE(nseq >= 1 && nseq <= 4096, "DeltaNet scan (conv): 1 <= nseq <= 4096");

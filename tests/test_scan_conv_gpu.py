@@ -90,3 +90,20 @@ def test_fused_conv_scan_rejects_other_tap_counts(clef):
         None, 0, 1, None, 3, None, 0, 0, None, None, None, 0, 0, None, 1, 64, 1, 1, 64, 64, 64, 1,
         None, 0, 0, None, 0, 0, None, None, None, 0, None)
     assert rc < 0
+
+
+@gpu
+def test_fused_conv_scan_rejects_v_conv_inside_mixed(clef):
+    """v_conv must not overlap the projection the prepare is reading."""
+    T, Hk, Hv, d = 64, 1, 2, 32
+    mixed, conv_w, g, beta, _, W = _inputs(3, T, Hk, Hv, d, torch.float16)
+    scan = clef.DeltaScan(d, d, "mixed")
+    n = clef.lib().clef_delta_scan_workspace(T, Hk, Hv, d, d, 64, scan.precision)
+    ws = torch.empty(n + 256, dtype=torch.uint8, device="cuda")
+    off = (-ws.data_ptr()) % 256
+    out = torch.empty((T, Hv, d), device="cuda")
+    rc = clef.lib().clef_delta_scan_conv(
+        mixed.data_ptr(), mixed.stride(0), 1, conv_w.data_ptr(), 4, None, 0, 0, mixed.data_ptr(),
+        g.data_ptr(), beta.data_ptr(), g.stride(0), 0, None, 1, T, Hk, Hv, d, d, 64, scan.precision,
+        None, 0, 0, out.data_ptr(), Hv * d, 0, None, None, ws.data_ptr() + off, n, None)
+    assert rc < 0 and "overlaps" in clef.last_error()
