@@ -6,9 +6,9 @@
 // A work-group of 8 waves (4 x 2, two per SIMD) computes a 256 x BN tile,
 // each wave 64 x BN/2 with v_mfma_f32_32x32x16_f16 (at most 128 accumulator
 // registers per wave, which the register allocator keeps in place).  K
-// advances in 64-element stages through two LDS buffers filled by
-// global->LDS DMA (global_load_lds_dwordx4, 1 KiB per wave instruction):
-// while a stage is multiplied the next one lands.
+// advances in 64-element stages through two LDS buffers (three for 128-wide
+// tiles) filled by global->LDS DMA (global_load_lds_dwordx4, 1 KiB per wave
+// instruction): while a stage is multiplied the next one or two land.
 // Rows are 128 bytes; the 16-byte chunk c of row r is stored at slot
 // c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit 16
 // distinct bank groups.  The DMA lanes pick their source chunk so that the
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) half_t smem[NS * (kStA + kStB)];
   auto sA = [&](int st) { return smem + st * kStA; };
   auto sB = [&](int st) { return smem + NS * kStA + st * kStB; };
-  static_assert(NS == 2, "two LDS stages");
+  static_assert(NS == 2 || NS == 3, "two or three LDS stages");
   static_assert(kWaves * 32 * WN * 4 <= (int)sizeof(smem), "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -282,7 +282,10 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
 template <int BN, int EPI>
 int launch(const GemmParams& p, hipStream_t s) {
   constexpr int VM = 4;
-  constexpr int NS = 2;
+  // three stages where they fit in LDS (128-wide tiles: 3 x 48 KiB): the
+  // DMA then runs two stages ahead (whole prefill 1.4% faster, interleaved
+  // A/B, all from the residual GEMMs)
+  constexpr int NS = BN == 128 ? 3 : 2;
   const int tiles_m = (p.M + kBM - 1) / kBM;
   const int tiles_n = EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   hipLaunchKernelGGL((gemm_f16_dma<BN, VM, NS, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
