@@ -52,6 +52,7 @@ SIGNATURES = {
                                     _p, _l, _p, _l, _i, _p, _p, _z, _p]),
     "clef_delta_scan_conv": (_i, [_p, _l, _i, _p, _i, _p, _i, _l, _p, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i,
                                   _i, _i, _p, _l, _i, _p, _l, _i, _p, _p, _p, _z, _p]),
+    "clef_silu_mul": (_i, [_p, _p, _p, _l, _i, _p]),
     "clef_gemm": (_i, [_p, _l, _p, _l, _p, _l, _i, _i, _i, _i, _i, _i, _p]),
     "clef_gemm_swiglu": (_i, [_p, _l, _p, _p, _l, _p, _l, _i, _i, _i, _i, _p]),
     "clef_rms_norm": (_i, [_p, _l, _i, _p, _p, _l, _i, _i, _i, _f, _p]),
@@ -358,6 +359,15 @@ def rms_norm(x, w, eps=1e-6, out_dtype=None):
     y = torch.empty((rows, width), dtype=out_dtype or x.dtype, device=x.device)
     _check(lib().clef_rms_norm(_ptr(x), _rows(x, "x"), _dt(x), _ptr(w), _ptr(y), width, _dt(y),
                                rows, width, float(eps), _stream()))
+    return y
+
+
+def silu_mul(gate, up):
+    """silu(gate) * up elementwise (clef_silu_mul): the unfused SwiGLU product."""
+    if gate.shape != up.shape or gate.dtype != up.dtype or not gate.is_contiguous() or not up.is_contiguous():
+        raise ClefError(-1, "gate and up must be contiguous tensors of one shape and dtype")
+    y = torch.empty_like(gate)
+    _check(lib().clef_silu_mul(_ptr(gate), _ptr(up), _ptr(y), gate.numel(), _dt(gate), _stream()))
     return y
 
 

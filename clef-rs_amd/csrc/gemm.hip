@@ -193,10 +193,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
           const int c = n0 + wn * (WN / 2) + j * 32 + ccol;
           if (r < p.M && c < p.N) {
             float out;
-            if (p.dtype_out == 1) {  // half roundings of neural.metal:35-42
-              const float g = round_to(acc[i][j][e], 1);
-              const float s = round_to(g / (1.0f + expf(-g)), 1);
-              out = s * round_to(acc[i][j + TN / 2][e], 1);
+            if (p.dtype_out == 1) {  // half roundings of neural.metal:35-42 (SiLU as gemm_f16.hip's)
+              const float g = static_cast<float>(to_f16(acc[i][j][e]));
+              const float s = static_cast<float>(to_f16(silu_hw(g)));
+              out = s * static_cast<float>(to_f16(acc[i][j + TN / 2][e]));
             } else {
               const float g = acc[i][j][e];
               out = (g / (1.0f + expf(-g))) * acc[i][j + TN / 2][e];

@@ -213,11 +213,14 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       if (EPI == 2) {
         const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
         const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
-        // half roundings of neural.metal:35-42
+        // half roundings of neural.metal:35-42; SiLU on the hardware exp2 and
+        // reciprocal (expf and an IEEE division cost ~1.8% of a prefill
+        // here), the same function as clef_silu_mul's, so fused and unfused
+        // agree bit for bit (neural.rs:484-492)
         auto sw = [](float gv, float uv) {
-          const float gh = static_cast<float>(static_cast<half_t>(gv));
-          const float sh = static_cast<float>(static_cast<half_t>(gh / (1.0f + expf(-gh))));
-          return sh * static_cast<float>(static_cast<half_t>(uv));
+          const float gh = static_cast<float>(to_f16(gv));
+          const float sh = static_cast<float>(to_f16(silu_hw(gh)));
+          return sh * static_cast<float>(to_f16(uv));
         };
         v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
       } else {

@@ -462,6 +462,20 @@ __global__ __launch_bounds__(256) void gated_rms128_kernel(const TOI* __restrict
   }
 }
 
+// ---- SwiGLU product, the unfused form of the f16 GEMM epilogue ---------------
+// f16: y = half(half(silu(g)) * u) with g, u f16 values (the product of two
+// f16 values is exact in f32, so y is rounded once); f32: silu(g) * u with
+// expf and an IEEE division, as the f32 epilogue.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const void* g, const void* u, void* y, int64_t n, int dt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float gv = ld(g, i, dt), uv = ld(u, i, dt);
+  if (dt == CLEF_F16)
+    st(y, i, dt, static_cast<float>(to_f16(silu_hw(gv))) * uv);
+  else
+    st(y, i, dt, (gv / (1.0f + expf(-gv))) * uv);
+}
+
 // ---- decay and write strength (qwen.rs:619-627) -----------------------------
 __global__ __launch_bounds__(256) void gates_kernel(const void* a, int64_t lda, const void* b,
                                                     int64_t ldb, int dti, const float* dt,
@@ -840,6 +854,14 @@ extern "C" int clef_delta_gates(const void* a, int64_t lda, const void* b, int64
   hipLaunchKernelGGL(gates_kernel, dim3((T * Hv + 255) / 256), dim3(256), 0, (hipStream_t)stream,
                      a, lda, b, ldb, dtype_in, dt, a_log, g, beta, T, Hv);
   return check_launch("delta_gates");
+}
+
+extern "C" int clef_silu_mul(const void* gate, const void* up, void* y, int64_t n, int dtype, void* stream) {
+  CLEF_REQUIRE(gate && up && y, "silu_mul: null pointer");
+  CLEF_REQUIRE(n >= 1 && n <= (int64_t(1) << 40) && dtype_ok(dtype), "silu_mul: size or dtype");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, gate, up,
+                     y, n, dtype);
+  return check_launch("silu_mul");
 }
 
 extern "C" int clef_gated_rms_silu(const void* o, int dtype_o, const void* z, int64_t ldz, int dtype_z,

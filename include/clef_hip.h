@@ -215,6 +215,15 @@ int clef_delta_gates_pack(const void* w_ab, int64_t ldw, int K, int Hv, int dtyp
 int clef_delta_gates_proj(const void* x, int64_t ldx, const void* packed, int K, int dtype, const float* dt,
                           const float* a_log, float* g, float* beta, int T, int Hv, void* stream);
 /*
+ * The unfused SwiGLU product (the gated_forward fallback of projection.rs:
+ * 67-81: silu(gate) * up on separate projections): y[i] = silu(gate[i]) *
+ * up[i] over n elements of dtype (all three arrays).  f16: the half roundings
+ * of neural.metal:35-42 with the same SiLU as clef_gemm_swiglu's f16
+ * epilogue, so clef_gemm_swiglu equals clef_gemm + clef_gemm + this bit for
+ * bit (the reference's fused-vs-unfused rule, neural.rs:484-492).
+ */
+int clef_silu_mul(const void* gate, const void* up, void* y, int64_t n, int dtype, void* stream);
+/*
  * Gated output norm, qwen.rs:671-676: per token and v-head row of `width`,
  * o is rounded to dtype_out (the scan output cast to the activation dtype),
  * RMS-normalised in f32 with w (no offset), rounded to dtype_out, multiplied

@@ -109,13 +109,18 @@ def test_swiglu_matches_half_rounding_steps_and_unfused_kernels(clef, M, N, K):
     wg = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
     wu = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
     y = clef.gemm_swiglu(x, wg, wu)
-    g = clef.gemm(x, wg).float()
-    u = clef.gemm(x, wu).float()
+    g16, u16 = clef.gemm(x, wg), clef.gemm(x, wu)
+    # the reference's rule: the fused kernel equals the unfused kernels
+    assert torch.equal(y, clef.silu_mul(g16, u16))
+    # the half-rounding steps with an exactly rounded SiLU: the hardware SiLU
+    # moves the rounded silu by one ulp in rare cases, which the product
+    # carries to at most two ulps of the output
+    g, u = g16.float(), u16.float()
     s = (g / (1.0 + torch.exp(-g))).half().float()
     unfused = (s * u).half()
     diff = (y.float() - unfused.float()).abs()
     ulp = unfused.float().abs().clamp(min=2.0 ** -14) * 2.0 ** -10
-    assert (diff <= ulp).all()
+    assert (diff <= 2 * ulp).all()
     assert (diff == 0).float().mean() > 0.999
     gr = (x.float() @ wg.float().T).half().float()
     ur = (x.float() @ wu.float().T).half().float()
