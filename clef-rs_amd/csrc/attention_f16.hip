@@ -364,7 +364,9 @@ __global__ __launch_bounds__(256) void attn_f16(AttnParams p) {
     lds_barrier();
   }
 
-  // ---- epilogue: y = round(round(O / l) * round(sigmoid(gate))).  O^T
+  // ---- epilogue: y = round(round(O / l) * round(sigmoid(gate))), the
+  // sigmoid on the hardware exp2 and reciprocal (the epilogue's vector ALU
+  // work is not hidden: one wave per SIMD).  O^T
   // accumulator e of tile t holds d = 32 t + 8 (e / 4) + 4 g + e % 4: four
   // consecutive features per (t, e / 4).  With 8-byte aligned gate and y
   // rows every gate read is issued before the first store (the loads would
@@ -378,8 +380,8 @@ __global__ __launch_bounds__(256) void attn_f16(AttnParams p) {
     half4 r;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float a = static_cast<float>(static_cast<half_t>(O[t][4 * blk + e] * inv));
-      const float sg = static_cast<float>(static_cast<half_t>(sigmoid(static_cast<float>(gv[e]))));
+      const float a = static_cast<float>(to_f16(O[t][4 * blk + e] * inv));
+      const float sg = static_cast<float>(to_f16(sigmoid_hw(static_cast<float>(gv[e]))));
       r[e] = static_cast<half_t>(a * sg);
     }
     return r;
