@@ -37,9 +37,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--profile", choices=("mixed", "f32"), default="mixed")
-    ap.add_argument("--cpu-tokens", type=int, default=1024,
+    ap.add_argument("--cpu-tokens", type=int, default=2048,
                     help="tokens of the bounded CPU-oracle sample (0 disables it)")
-    ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--cpu-runs", type=int, default=4)
     ap.add_argument("--ragged", type=int, default=1,
                     help="also time the ragged batch: 32 requests of U[128, 4096] tokens behind one shared "
                          "512-token prefix (0: skip)")
