@@ -858,7 +858,8 @@ extern "C" int clef_delta_gates(const void* a, int64_t lda, const void* b, int64
 
 extern "C" int clef_silu_mul(const void* gate, const void* up, void* y, int64_t n, int dtype, void* stream) {
   CLEF_REQUIRE(gate && up && y, "silu_mul: null pointer");
-  CLEF_REQUIRE(n >= 1 && n <= (int64_t(1) << 40) && dtype_ok(dtype), "silu_mul: size or dtype");
+  // (one element per thread: at most 2^31 - 1 work-groups of 256)
+  CLEF_REQUIRE(n >= 1 && n <= int64_t(0x7fffffff) * 256 && dtype_ok(dtype), "silu_mul: size or dtype");
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, gate, up,
                      y, n, dtype);
   return check_launch("silu_mul");
