@@ -128,8 +128,8 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the scan shards over v-heads and the GEMMs over columns; see DESIGN.md). "
+        print("bench.py measures one MI355X: there is no multi-GPU path "
+              "(the scan would shard over v-heads and the GEMMs over columns). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 

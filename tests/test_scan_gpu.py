@@ -1,6 +1,6 @@
 """Parity of the gfx950 chunked DeltaNet scan against the CPU oracle.
 
-Bars (north star): strict f32 profile rtol 1e-4 / atol 1e-5 against the CPU
+Bars: strict f32 profile rtol 1e-4 / atol 1e-5 against the CPU
 F32 recurrence (qwen.rs:826-882); mixed f16-MFMA profile rtol 2e-2 with an
 absolute floor of 2e-2 * max|expected| (elementwise relative error is
 meaningless at near-zero outputs).  Capture/resume at chunk-aligned
@@ -34,7 +34,7 @@ def _check(actual, expected, precision):
         _close(actual, expected, MIXED_RTOL, MIXED_RTOL * np.abs(expected).max())
 
 
-def baseline_inputs(seed, T, Hk, Hv, dk, dv, dtype=torch.float32, device="cuda"):
+def case_inputs(seed, T, Hk, Hv, dk, dv, dtype=torch.float32, device="cuda"):
     import workloads
     return workloads.scan_inputs(seed, T, Hk, Hv, dk, dv, dtype=dtype, device=device)
 
@@ -54,7 +54,7 @@ def clef():
 @pytest.mark.parametrize("precision", ["strict", "mixed"])
 def test_scan_small_config_seed0(clef, precision):
     """B=1, T=256, H=4, dk=dv=64, chunk 64, f32 inputs, zero initial state."""
-    q, k, v, g, beta = baseline_inputs(0, 256, 4, 4, 64, 64)
+    q, k, v, g, beta = case_inputs(0, 256, 4, 4, 64, 64)
     out, _, final = clef.DeltaScan(64, 64, precision).prefill(q, k, v, g, beta)
     eo, _, ef = oracle.delta_scan(*_np(q, k, v, g, beta))
     _check(out.cpu().numpy(), eo, precision)
@@ -101,7 +101,7 @@ def test_scan_chunk_candidate_shapes(clef, T, H, dk, dv, decay):
 @pytest.mark.parametrize("precision", ["strict", "mixed"])
 def test_scan_gqa_initial_state_and_f16_io(clef, precision):
     T, Hk, Hv, dk, dv = 200, 2, 6, 64, 48
-    q, k, v, g, beta = baseline_inputs(11, T, Hk, Hv, dk, dv, dtype=torch.float16)
+    q, k, v, g, beta = case_inputs(11, T, Hk, Hv, dk, dv, dtype=torch.float16)
     init = torch.randn((Hv, dk, dv), device="cuda") * 0.1
     out, _, final = clef.DeltaScan(dk, dv, precision).prefill(q, k, v, g, beta, initial=init,
                                                               out_dtype=torch.float16)
@@ -137,7 +137,7 @@ def test_scan_strided_views_of_packed_projection(clef):
 @pytest.mark.parametrize("precision", ["strict", "mixed"])
 def test_scan_capture_and_resume(clef, precision):
     T, H, dk, dv = 257, 2, 128, 128
-    q, k, v, g, beta = baseline_inputs(5, T, H, H, dk, dv)
+    q, k, v, g, beta = case_inputs(5, T, H, H, dk, dv)
     scan = clef.DeltaScan(dk, dv, precision)
     full, _, final = scan.prefill(q, k, v, g, beta)
     for boundary in (1, 16, 64, 128, 256):
@@ -161,7 +161,7 @@ def test_scan_capture_and_resume(clef, precision):
 @pytest.mark.parametrize("precision", ["strict", "mixed"])
 def test_scan_full_layer_config(clef, precision):
     """T=4096, Hk=16, Hv=32, dk=dv=128, f16 q/k/v/g/beta, f32 state and output."""
-    q, k, v, g, beta = baseline_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16)
+    q, k, v, g, beta = case_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16)
     out, _, final = clef.DeltaScan(128, 128, precision).prefill(q, k, v, g, beta)
     eo, _, ef = oracle.delta_scan(*_np(q, k, v, g, beta))
     _check(out.cpu().numpy(), eo, precision)
@@ -170,7 +170,7 @@ def test_scan_full_layer_config(clef, precision):
 
 @gpu
 def test_scan_is_deterministic(clef):
-    q, k, v, g, beta = baseline_inputs(9, 1000, 4, 8, 128, 128, dtype=torch.float16)
+    q, k, v, g, beta = case_inputs(9, 1000, 4, 8, 128, 128, dtype=torch.float16)
     scan = clef.DeltaScan(128, 128, "mixed")
     a = scan.prefill(q, k, v, g, beta)[0].clone()
     b = scan.prefill(q, k, v, g, beta)[0]
@@ -189,7 +189,7 @@ def test_scan_varlen_matches_per_sequence_oracle(clef, precision, shared):
     Hk, Hv, dk, dv = 2, 4, 64, 48
     T = sum(lens)
     dt = torch.float32 if precision == "strict" else torch.float16
-    q, k, v, g, beta = baseline_inputs(5, T, Hk, Hv, dk, dv, dtype=dt)
+    q, k, v, g, beta = case_inputs(5, T, Hk, Hv, dk, dv, dtype=dt)
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
     gen = torch.Generator(device="cuda").manual_seed(9)
     nseq = len(lens)
