@@ -184,3 +184,29 @@ def test_packed_gemm_rejects_swiglu(clef):
     rc = clef.lib().clef_gemm_packed(ctypes.c_void_p(16), 64, ctypes.c_void_p(16), ctypes.c_void_p(16), 64, 4, 4,
                                      64, 1, 1, 2, None)
     assert rc != 0
+
+
+@gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_silu_mul_matches_the_formula(clef, dt):
+    """clef_silu_mul: f32 as silu(g) * u; f16 with the SwiGLU's half roundings,
+    the SiLU within one f16 ulp of the exactly rounded one."""
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    g = (4 * torch.randn(100_003, generator=gen, device="cuda")).to(dt)
+    u = torch.randn(100_003, generator=gen, device="cuda").to(dt)
+    y = clef.silu_mul(g, u).float()
+    gf, uf = g.float(), u.float()
+    if dt == torch.float32:
+        torch.testing.assert_close(y, gf / (1 + torch.exp(-gf)) * uf, rtol=1e-6, atol=1e-7)
+    else:
+        ref = ((gf / (1 + torch.exp(-gf))).half().float() * uf).half().float()
+        ulp = ref.abs().clamp(min=2.0 ** -14) * 2.0 ** -10
+        assert ((y - ref).abs() <= 2 * ulp).all()
+        assert (y == ref).float().mean() > 0.999
+
+
+def test_silu_mul_rejects_bad_arguments(clef):
+    """Validation before any launch (no GPU needed)."""
+    assert clef.lib().clef_silu_mul(None, None, None, 16, 1, None) < 0
+    assert clef.lib().clef_silu_mul(1, 1, 1, 0, 1, None) < 0
+    assert clef.lib().clef_silu_mul(1, 1, 1, 16, 7, None) < 0

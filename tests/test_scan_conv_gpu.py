@@ -39,7 +39,8 @@ def _split(y, T, Hk, Hv, d):
 @gpu
 @pytest.mark.parametrize("precision", ["strict", "mixed"])
 @pytest.mark.parametrize("T,Hk,Hv,d,hist_rows,capture", [(300, 2, 4, 64, 0, 0), (200, 2, 4, 64, 3, 77),
-                                                         (65, 1, 2, 32, 2, 65), (4096, 16, 32, 128, 0, 0)])
+                                                         (65, 1, 2, 32, 2, 65), (100, 2, 4, 40, 1, 0),
+                                                         (3, 1, 1, 8, 3, 2), (4096, 16, 32, 128, 0, 0)])
 def test_fused_conv_scan_equals_conv_then_scan(clef, precision, T, Hk, Hv, d, hist_rows, capture):
     dt = torch.float32 if precision == "strict" else torch.float16
     mixed, conv_w, g, beta, hist, W = _inputs(T + d, T, Hk, Hv, d, dt)
