@@ -110,11 +110,8 @@ def ragged_batch(model, cfg, args, torch, np, dev):
     history and attention K/V are computed once, before timing; a step is one
     ragged prefill of all requests (cu_seqlens packing, each request with its
     own state and causal mask)."""
-    rng = np.random.default_rng(4)
-    lens = rng.integers(128, 4097, 32)
-    prefix_ids = rng.integers(0, cfg["vocab_size"], 512)
-    req_ids = rng.integers(0, cfg["vocab_size"], int(lens.sum()))
-    cu = np.concatenate([[0], np.cumsum(lens)])
+    import workloads
+    prefix_ids, lens, req_ids, cu = workloads.ragged_workload(cfg, seed=4)
     _, state = model.prefill(np.concatenate([prefix_ids, req_ids[:1]]), capture=512)
     hidden = torch.empty((int(lens.sum()), cfg["hidden_size"]), dtype=torch.float32, device=dev)
     ms = event_ms(lambda: model.prefill_varlen(req_ids, cu, initial=state, hidden=hidden), args.steps,

@@ -48,6 +48,7 @@ SIGNATURES = {
     "clef_delta_scan": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _i, _i, _i,
                              _p, _i, _p, _l, _i, _p, _p, _p, _z, _p]),
     "clef_delta_scan_varlen_workspace": (_z, [_i] * 8),
+    "clef_ragged_plan": (_i, [_p, _i, _i, _i, _p, _p, _z]),
     "clef_delta_scan_varlen": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i,
                                     _p, _l, _p, _l, _i, _p, _p, _z, _p]),
     "clef_delta_scan_conv": (_i, [_p, _l, _i, _p, _i, _p, _i, _l, _p, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i,
@@ -60,7 +61,7 @@ SIGNATURES = {
     "clef_delta_gates": (_i, [_p, _l, _p, _l, _i, _p, _p, _p, _p, _i, _i, _p]),
     "clef_gemm_pack_bytes": (_z, [_i, _i]),
     "clef_gemm_pack": (_i, [_p, _l, _i, _i, _i, _p, _p]),
-    "clef_gemm_packed": (_i, [_p, _l, _p, _p, _l, _i, _i, _i, _i, _i, _i, _p]),
+    "clef_gemm_packed": (_i, [_p, _l, _p, _z, _p, _l, _i, _i, _i, _i, _i, _i, _p]),
     "clef_delta_gates_pack_bytes": (_z, [_i, _i]),
     "clef_delta_gates_pack": (_i, [_p, _l, _i, _i, _i, _p, _p]),
     "clef_delta_gates_proj": (_i, [_p, _l, _p, _i, _i, _p, _p, _p, _p, _i, _i, _p]),
@@ -279,6 +280,21 @@ def delta_scan_conv(scan, mixed, Hk, Hv, conv_w, g, beta, history=None, cu_seqle
     return out, vconv, captured, final
 
 
+def ragged_plan(cu_seqlens, T, unit):
+    """Host evaluation of a ragged batch's launch tables (clef_ragged_plan):
+    returns (spans [nseq + 1], units [n, 2]) as numpy int32 arrays."""
+    import numpy as np
+    cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
+    nseq = int(cu.shape[0]) - 1
+    spans = np.zeros(nseq + 1, np.int32)
+    cap = (T + unit - 1) // unit + nseq
+    table = np.zeros((cap, 2), np.int32)
+    n = lib().clef_ragged_plan(cu.ctypes.data, nseq, T, unit, spans.ctypes.data, table.ctypes.data, cap)
+    if n < 0:
+        raise ClefError(n, last_error())
+    return spans, table[:n].copy()
+
+
 def _rows(t, name):
     if t.dim() != 2 or t.stride(1) != 1 or not t.is_cuda:
         raise ClefError(-1, f"{name} must be a row-major 2-D device tensor")
@@ -346,8 +362,8 @@ def gemm_packed(x, pw: PackedWeights, out=None, out_dtype=None, residual=None):
     else:
         y = out if out is not None else torch.empty((M, pw.N), dtype=out_dtype or x.dtype, device=x.device)
         epi, dto = EPI_STORE, _dt(y)
-    _check(lib().clef_gemm_packed(_ptr(x), _rows(x, "x"), _ptr(pw.buffer), _ptr(y), _rows(y, "y"), M, pw.N, K,
-                                  _dt(x), dto, epi, _stream()))
+    _check(lib().clef_gemm_packed(_ptr(x), _rows(x, "x"), _ptr(pw.buffer), pw.buffer.numel(), _ptr(y),
+                                  _rows(y, "y"), M, pw.N, K, _dt(x), dto, epi, _stream()))
     return y
 
 
@@ -523,22 +539,33 @@ class LayerWeights(C.Structure):
     _fields_ = [("kind", C.c_int)] + [(n, C.c_void_p) for n in _LW]
 
 
+class Control(C.Structure):
+    _fields_ = [("cancel", C.POINTER(C.c_int32)), ("deadline", C.c_double)]
+
+
 SIGNATURES.update({
     "clef_backbone_create": (_i, [C.POINTER(BackboneConfig), C.POINTER(LayerWeights), _p, _p,
                                   C.POINTER(C.c_void_p)]),
     "clef_backbone_destroy": (None, [_p]),
     "clef_backbone_workspace": (_z, [_p, _i, _i]),
     "clef_backbone_prefix_bytes": (_z, [_p, _i]),
-    "clef_backbone_prefill": (_i, [_p, C.POINTER(C.c_int32), _i, _p, _i, _i, _p, _p, _p, _z, _p]),
+    "clef_backbone_prefill": (_i, [_p, C.POINTER(C.c_int32), _i, _p, _i, _z, _i, _p, _z, _p, _p, _z, _p]),
     "clef_backbone_varlen_workspace": (_z, [_p, _i, _i, _i]),
-    "clef_backbone_prefill_varlen": (_i, [_p, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _i, _p, _i, _p, _p, _z,
-                                          _p]),
+    "clef_backbone_prefill_varlen": (_i, [_p, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _i, _p, _i, _z, _p, _p,
+                                          _z, _p]),
+    "clef_backbone_set_control": (_i, [_p, C.POINTER(Control)]),
+    "clef_monotonic_seconds": (_d, []),
     "clef_backbone_enable_timing": (_i, [_p, _i]),
     "clef_backbone_timings": (_i, [_p, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double),
                                    C.POINTER(C.c_double)]),
 })
 
 CATEGORIES = ("gemm", "scan", "attention", "conv", "norm", "other")
+CANCELLED, DEADLINE_EXCEEDED = -20, -21
+
+
+def monotonic_seconds() -> float:
+    return lib().clef_monotonic_seconds()
 
 
 class PrefixState:
@@ -644,6 +671,19 @@ class Backbone:
     def enable_timing(self, enable=True):
         _check(lib().clef_backbone_enable_timing(self._h, int(enable)))
 
+    def set_control(self, cancel=None, deadline=0.0):
+        """Cooperative cancellation / deadline (Control, models/mod.rs:45-59).
+        cancel: a ctypes.c_int32 flag another thread may set (kept referenced
+        here); deadline: absolute seconds on monotonic_seconds()'s clock, 0 =
+        none.  set_control() with no arguments clears it."""
+        self._cancel = cancel
+        if cancel is None and not deadline:
+            _check(lib().clef_backbone_set_control(self._h, None))
+            return
+        c = Control(C.cast(C.pointer(cancel), C.POINTER(C.c_int32)) if cancel is not None else None,
+                    float(deadline))
+        _check(lib().clef_backbone_set_control(self._h, C.byref(c)))
+
     def timings(self):
         """Per-category {ms, launches, flops, bytes} of the prefills since the last call."""
         n = len(CATEGORIES)
@@ -679,9 +719,10 @@ class Backbone:
         ws = self._workspace(T, prefix, dev)
         _check(lib().clef_backbone_prefill(
             self._h, ids.ctypes.data_as(C.POINTER(C.c_int32)), T,
-            _ptr(initial.buffer) if initial is not None else None, prefix, int(capture),
-            _ptr(saved.buffer) if saved is not None else None, _ptr(hidden), _ptr(ws), ws.numel(),
-            _stream()))
+            _ptr(initial.buffer) if initial is not None else None, prefix,
+            initial.bytes() if initial is not None else 0, int(capture),
+            _ptr(saved.buffer) if saved is not None else None, saved.bytes() if saved is not None else 0,
+            _ptr(hidden), _ptr(ws), ws.numel(), _stream()))
         return hidden, saved
 
     def prefill_varlen(self, ids, cu_seqlens, initial: PrefixState = None, hidden=None):
@@ -703,8 +744,9 @@ class Backbone:
             self._ws = torch.empty(n, dtype=torch.uint8, device=dev)
         _check(lib().clef_backbone_prefill_varlen(
             self._h, ids.ctypes.data_as(C.POINTER(C.c_int32)), cu.ctypes.data_as(C.POINTER(C.c_int32)), nseq,
-            _ptr(initial.buffer) if initial is not None else None, prefix, _ptr(hidden), _ptr(self._ws),
-            self._ws.numel(), _stream()))
+            _ptr(initial.buffer) if initial is not None else None, prefix,
+            initial.bytes() if initial is not None else 0, _ptr(hidden), _ptr(self._ws), self._ws.numel(),
+            _stream()))
         return hidden
 
 

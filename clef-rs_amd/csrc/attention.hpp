@@ -21,6 +21,8 @@ struct AttnParams {
   const int* cu_q;   // [nseq + 1] (device)
   int2* pairs;       // [blocks / heads] {sequence, query tile}, most keys first
   int* npairs;       // valid entries of pairs
+  int* keys;         // [tiles] key count per query tile (table scratch)
+  int* spans;        // [nseq + 1] cu_q made monotone in [0, T] (ragged.hpp)
   int nseq;
   const void* pk;    // [kvh][ldpk][d] or null
   const void* pvt;   // [kvh][d][ldpv]
@@ -32,7 +34,7 @@ struct AttnParams {
 // device tables of a ragged batch (workspace: attn_tables_bytes)
 size_t attn_tables_bytes(int T, int nseq);
 void attn_carve_tables(AttnParams& p, void* ws);
-int attn_f16_tables(const AttnParams& p, hipStream_t s);
+int attn_f16_tables(AttnParams& p, hipStream_t s);
 
 // f16 flash-attention path (MFMA 32x32x16, LDS-DMA key/value tiles); false if
 // the shape is outside what it handles, in which case nothing is launched.

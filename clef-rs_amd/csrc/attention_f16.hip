@@ -21,6 +21,7 @@
 // 2^8.  Both O and the row sum use the same reference, so O / l is the
 // softmax average exactly as in the eager formulation.
 #include "attention.hpp"
+#include "ragged.hpp"
 #include "common.hpp"
 
 namespace clef {
@@ -423,54 +424,36 @@ __global__ __launch_bounds__(256) void attn_f16(AttnParams p) {
   }  // work items (the last key tile ended with a barrier: LDS is free)
 }
 
-// Query tiles of a ragged batch (one work-group): per sequence its tiles of
-// 128 queries, ranked by key count (most first, ties in sequence order) for
-// a longest-first launch.  Offsets are clamped to [0, T].  Beyond 8192 tiles
-// the ranking is skipped (sequence order).
-__global__ __launch_bounds__(256) void attn_tables(const int* __restrict__ cu, int nseq, int T, int np,
-                                                   int2* __restrict__ pairs, int* __restrict__ npairs,
-                                                   int* __restrict__ keys) {
+// Query tiles of a ragged batch (one work-group, ragged.hpp): the monotone
+// spans (written to `spans`, which the attention kernel then reads as its
+// sequence offsets), and per sequence its tiles of 128 queries ranked by key
+// count (most first, ties in sequence order) for a longest-first launch;
+// beyond 8192 tiles in sequence order.  Any offset table keeps the pair
+// table inside its T/128 + nseq entries.
+__global__ __launch_bounds__(kTabThreads) void attn_tables(const int* __restrict__ cu, int nseq, int T, int np,
+                                                           int* __restrict__ spans, int2* __restrict__ pairs,
+                                                           int* __restrict__ npairs, int* __restrict__ keys) {
+  __shared__ int s_part[kTabThreads];
+  __shared__ int s_R[kMaxRaggedSeq + 1];
   __shared__ int s_total;
   const int tid = threadIdx.x;
-  const int per = (nseq + 255) / 256;  // consecutive sequences per thread
-  const int s0 = min(tid * per, nseq), s1 = min(s0 + per, nseq);
-  auto length = [&](int s) {
-    const int a = min(max(cu[s], 0), T);
-    return min(max(cu[s + 1], a), T) - a;
-  };
-  auto tiles = [&](int s) { return (length(s) + 127) / 128; };
-  int first = 0;
-  for (int s = 0; s < s0; ++s) first += tiles(s);
-  if (tid == 0) {
-    int t = 0;
-    for (int s = 0; s < nseq; ++s) t += tiles(s);
-    s_total = t;
-    *npairs = t;
-  }
-  int f = first;
-  for (int s = s0; s < s1; ++s) {  // key count of each tile: prefix + its last query's causal reach
-    const int len = length(s), nt = tiles(s);
-    for (int t = 0; t < nt; ++t) keys[f + t] = np + min(128 * (t + 1), len);
-    f += nt;
-  }
+  const Ragged g{cu, nseq, T, s_part, s_R};
+  rg_spans_1(g, tid);
+  __syncthreads();
+  rg_spans_2(g, tid);
+  __syncthreads();
+  rg_spans_3(g, tid);
+  __syncthreads();
+  for (int j = tid; j <= nseq; j += kTabThreads) spans[j] = s_R[j];
+  rg_count_4(g, tid, 128);
+  __syncthreads();
+  rg_count_5(g, tid, &s_total);
+  __syncthreads();
+  if (tid == 0) *npairs = s_total;
+  rg_attn_6(g, tid, 128, np, keys);
   __threadfence_block();
   __syncthreads();
-  const int total = s_total;
-  f = first;
-  for (int s = s0; s < s1; ++s) {
-    const int nt = tiles(s);
-    for (int t = 0; t < nt; ++t) {
-      const int i = f + t;
-      int rank = i;
-      if (total <= 8192) {
-        rank = 0;
-        const int ki = keys[i];
-        for (int j = 0; j < total; ++j) rank += (keys[j] > ki) || (keys[j] == ki && j < i);
-      }
-      pairs[rank] = make_int2(s, t);
-    }
-    f += nt;
-  }
+  rg_attn_7(g, tid, 128, s_total, keys, reinterpret_cast<int*>(pairs));
 }
 
 // work-groups resident at once (CUs x occupancy of the instance), per device
@@ -503,24 +486,35 @@ int launch(const AttnParams& p0, hipStream_t s) {
 
 }  // namespace
 
+// Workspace: pairs [tiles] int2, keys [tiles] int, the pair count, spans
+// [nseq + 1] int, each region 256-byte aligned.
+namespace {
+size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+}  // namespace
+
 size_t attn_tables_bytes(int T, int nseq) {
   const size_t tiles = (size_t)(T + 127) / 128 + nseq;
-  return ((tiles * sizeof(int2) + 255) & ~(size_t)255) + ((tiles * sizeof(int) + 255) & ~(size_t)255) + 256;
+  return al256(tiles * sizeof(int2)) + al256(tiles * sizeof(int)) + 256 + al256(((size_t)nseq + 1) * sizeof(int));
 }
 
 void attn_carve_tables(AttnParams& p, void* ws) {
   const size_t tiles = (size_t)(p.qn + 127) / 128 + p.nseq;
   char* b = static_cast<char*>(ws);
   p.pairs = reinterpret_cast<int2*>(b);
-  b += (tiles * sizeof(int2) + 255) & ~(size_t)255;
-  p.npairs = reinterpret_cast<int*>(b + ((tiles * sizeof(int) + 255) & ~(size_t)255));
+  b += al256(tiles * sizeof(int2));
+  p.keys = reinterpret_cast<int*>(b);
+  b += al256(tiles * sizeof(int));
+  p.npairs = reinterpret_cast<int*>(b);
+  p.spans = reinterpret_cast<int*>(b + 256);
 }
 
-int attn_f16_tables(const AttnParams& p, hipStream_t s) {
-  const size_t tiles = (size_t)(p.qn + 127) / 128 + p.nseq;
-  int* keys = reinterpret_cast<int*>(reinterpret_cast<char*>(p.pairs) + ((tiles * sizeof(int2) + 255) & ~(size_t)255));
-  hipLaunchKernelGGL(attn_tables, dim3(1), dim3(256), 0, s, p.cu_q, p.nseq, p.qn, p.np, p.pairs, p.npairs, keys);
-  return check_launch("attention tables");
+int attn_f16_tables(AttnParams& p, hipStream_t s) {
+  if (p.nseq < 1 || p.nseq > kMaxRaggedSeq) return fail(-1, "attention: 1..4096 sequences");
+  hipLaunchKernelGGL(attn_tables, dim3(1), dim3(kTabThreads), 0, s, p.cu_q, p.nseq, p.qn, p.np, p.spans, p.pairs,
+                     p.npairs, p.keys);
+  if (int rc = check_launch("attention tables")) return rc;
+  p.cu_q = p.spans;  // the attention kernel reads the monotone spans
+  return 0;
 }
 
 bool attn_f16_ok(const AttnParams& p) {

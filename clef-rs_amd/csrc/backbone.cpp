@@ -5,6 +5,8 @@
 // values on the host; the only host/device transfer is the token ids.
 #include <hip/hip_runtime.h>
 
+#include <time.h>
+
 #include <cstring>
 #include <memory>
 #include <new>
@@ -79,6 +81,8 @@ struct clef_backbone {
   // f16 profile: the a/b projections run fused with the gates
   // (clef_delta_gates_proj), so the in-projection GEMM covers [qkv | z] only
   bool ab_fused = false;
+  // cooperative cancellation / deadline (clef_backbone_set_control)
+  clef_control control{nullptr, 0.0};
 };
 
 namespace clef {
@@ -98,6 +102,15 @@ int hip_fail(hipError_t e, const char* what) {
     hipError_t e_ = (expr);                          \
     if (e_ != hipSuccess) return hip_fail(e_, what); \
   } while (0)
+
+// Control::check (models/mod.rs:49-58): cancellation first, then the deadline.
+int control_check(const clef_backbone* b) {
+  const clef_control& c = b->control;
+  if (c.cancel && __atomic_load_n(c.cancel, __ATOMIC_ACQUIRE) != 0) return fail(CLEF_CANCELLED, "prefill cancelled");
+  if (c.deadline > 0.0 && clef_monotonic_seconds() >= c.deadline)
+    return fail(CLEF_DEADLINE_EXCEEDED, "prefill deadline exceeded");
+  return 0;
+}
 
 struct Workspace {
   int32_t* ids;
@@ -125,6 +138,14 @@ struct Workspace {
 };
 
 size_t elt(int dtype) { return dtype == CLEF_F32 ? 4 : 2; }
+
+// A ragged batch runs its attention one sequence at a time over copied
+// [prefix; own] keys in the f32 profile, and in the mixed profile when the
+// shared prefix is not a multiple of 8 tokens (the packed kernel reads
+// 8-key runs that must not straddle the prefix / own boundary).
+bool varlen_per_sequence_attention(const clef_backbone* b, int prefix) {
+  return b->ad == CLEF_F32 || prefix % 8 != 0;
+}
 
 // nseq > 0: a ragged batch of nseq sequences, T tokens in all, each after the
 // same `prefix` cached tokens (which stay in the prefix state: kh / vt hold
@@ -168,7 +189,7 @@ size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base
     W.cu = static_cast<int32_t*>(take(sizeof(int32_t) * (nseq + 1)));
     W.attn_ws_bytes = clef_attention_varlen_workspace(T, nseq);
     W.attn_ws = take(W.attn_ws_bytes);
-    if (b->ad == CLEF_F32) {
+    if (varlen_per_sequence_attention(b, prefix)) {
       W.ldvs = static_cast<int>(((prefix + T + 63) / 64) * 64);
       W.kseq = take(a * (size_t)c.kv_heads * (prefix + T) * c.head_dim);
       W.vseq = take(a * (size_t)c.kv_heads * c.head_dim * W.ldvs);
@@ -423,18 +444,37 @@ extern "C" size_t clef_backbone_prefix_bytes(const clef_backbone* b, int tokens)
   return prefix_layout(b, tokens, nullptr, nullptr);
 }
 
+extern "C" double clef_monotonic_seconds(void) {
+  timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return static_cast<double>(ts.tv_sec) + 1e-9 * static_cast<double>(ts.tv_nsec);
+}
+
+extern "C" int clef_backbone_set_control(clef_backbone* b, const clef_control* control) {
+  CLEF_REQUIRE(b, "control: null backbone");
+  b->control = control ? *control : clef_control{nullptr, 0.0};
+  return 0;
+}
+
 extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T, const void* initial,
-                                     int initial_tokens, int capture, void* saved, float* hidden,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+                                     int initial_tokens, size_t initial_bytes, int capture, void* saved,
+                                     size_t saved_bytes, float* hidden, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
   CLEF_REQUIRE(b && ids && hidden && workspace, "prefill: null argument");
+  CLEF_TRY(control_check(b));  // qwen.rs:344
   const clef_backbone_config& c = b->c;
   const int offset = initial ? initial_tokens : 0;
-  // request validation, qwen.rs:345-359
+  // request validation, qwen.rs:345-359 (a state of another shape: :355)
   CLEF_REQUIRE(T >= 1 && offset >= 0 && (!initial || offset >= 1) && (int64_t)offset + T <= c.max_tokens,
                "prefill boundary or vocabulary");
   CLEF_REQUIRE(capture >= 0 && (capture == 0 || capture < T) && !(initial && capture) &&
                    (capture == 0 || saved),
                "prefill boundary or vocabulary");
+  CLEF_REQUIRE(!initial || initial_bytes == prefix_layout(b, offset, nullptr, nullptr),
+               "prefill boundary or vocabulary: the initial state's size does not match this backbone at "
+               "initial_tokens");
+  CLEF_REQUIRE(!capture || saved_bytes >= prefix_layout(b, capture, nullptr, nullptr),
+               "prefill: the capture buffer is smaller than clef_backbone_prefix_bytes(capture)");
   for (int t = 0; t < T; ++t) CLEF_REQUIRE(ids[t] >= 0 && ids[t] < c.vocab, "prefill boundary or vocabulary");
   const size_t need = carve(b, T, offset, nullptr, nullptr);
   char* base = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(workspace) + 255) & ~static_cast<uintptr_t>(255));
@@ -465,6 +505,7 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
 
   for (int li = 0; li < c.n_layers; ++li) {
     const LayerState& L = b->layers[li];
+    CLEF_TRY(control_check(b));  // qwen.rs:380
     TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
@@ -574,13 +615,17 @@ extern "C" size_t clef_backbone_varlen_workspace(const clef_backbone* b, int T, 
 // for every request, prefix_cache.rs:135-177): each sequence's hidden states
 // equal clef_backbone_prefill of its ids resumed from `initial`.
 extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids, const int32_t* cu_seqlens,
-                                            int nseq, const void* initial, int initial_tokens, float* hidden,
-                                            void* workspace, size_t workspace_bytes, void* stream) {
+                                            int nseq, const void* initial, int initial_tokens, size_t initial_bytes,
+                                            float* hidden, void* workspace, size_t workspace_bytes, void* stream) {
   CLEF_REQUIRE(b && ids && cu_seqlens && hidden && workspace, "prefill: null argument");
+  CLEF_TRY(control_check(b));
   CLEF_REQUIRE(nseq >= 1 && nseq <= 4096 && cu_seqlens[0] == 0, "prefill: 1..4096 sequences from offset 0");
   const clef_backbone_config& c = b->c;
   const int offset = initial ? initial_tokens : 0;
   CLEF_REQUIRE(offset >= 0 && (!initial || offset >= 1), "prefill boundary or vocabulary");
+  CLEF_REQUIRE(!initial || initial_bytes == prefix_layout(b, offset, nullptr, nullptr),
+               "prefill boundary or vocabulary: the initial state's size does not match this backbone at "
+               "initial_tokens");
   for (int s = 0; s < nseq; ++s)
     CLEF_REQUIRE(cu_seqlens[s + 1] > cu_seqlens[s] && (int64_t)offset + cu_seqlens[s + 1] - cu_seqlens[s] <= c.max_tokens,
                  "prefill: every sequence needs 1..max_tokens - prefix tokens");
@@ -622,6 +667,7 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
 
   for (int li = 0; li < c.n_layers; ++li) {
     const LayerState& L = b->layers[li];
+    CLEF_TRY(control_check(b));  // qwen.rs:380
     TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
@@ -670,7 +716,7 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
                                        c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
       TIMED(CLEF_CAT_OTHER, 0, 2.0 * da * T * kvh * d,
             clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, 0, s));
-      if (ad == CLEF_F16) {
+      if (!varlen_per_sequence_attention(b, offset)) {
         TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pairs, da * (3.0 * T * heads * d + 2.0 * (T + offset) * kvh * d),
               clef_attention_gated_varlen(w.qh, T, w.kh, T, w.vt, w.ldv, w.cu, nseq, T,
                                           initial ? init.key[li] : nullptr, offset,
@@ -678,7 +724,7 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
                                           proj + a * d, NA, 2 * d, w.gated, (int64_t)heads * d, w.attn_ws,
                                           w.attn_ws_bytes, s));
       } else {
-        // f32 profile: one launch per sequence over [prefix; own] keys
+        // one launch per sequence over [prefix; own] keys
         for (int q = 0; q < nseq; ++q) {
           const int t0 = cu_seqlens[q], Lq = cu_seqlens[q + 1] - t0, kn = offset + Lq;
           for (int gk = 0; gk < kvh; ++gk) {

@@ -66,12 +66,16 @@ extern "C" int clef_gemm_pack(const void* w, int64_t ldw, int N, int K, int dtyp
   return clef::gemm_pack_f16_launch(w, ldw, N, K, packed, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, void* y, int64_t ldy, int M, int N,
-                                int K, int dtype_in, int dtype_out, int epilogue, void* stream) {
+extern "C" int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, size_t packed_bytes, void* y,
+                                int64_t ldy, int M, int N, int K, int dtype_in, int dtype_out, int epilogue,
+                                void* stream) {
   if (ldx == 0) ldx = K;
   if (ldy == 0) ldy = N;
   if (int rc = gemm_checks(x, ldx, packed, K, nullptr, y, ldy, M, N, K, dtype_in, dtype_out)) return rc;
   CLEF_REQUIRE(dtype_in == CLEF_F16, "GEMM (packed): f16 operands only");
+  // every packed-weight read then stays inside the buffer
+  CLEF_REQUIRE(packed_bytes != 0 && packed_bytes == clef_gemm_pack_bytes(N, K),
+               "GEMM (packed): packed_bytes does not match clef_gemm_pack_bytes(N, K)");
   CLEF_REQUIRE(epilogue == CLEF_EPI_STORE || epilogue == CLEF_EPI_RESIDUAL,
                "GEMM (packed): store or residual epilogue (SwiGLU: clef_gemm_swiglu)");
   CLEF_REQUIRE(K % 64 == 0 && vec_ok(x, ldx, packed, K, nullptr, K, dtype_in) && (int64_t)M * ldx < (int64_t(1) << 31),

@@ -4,9 +4,11 @@
 
 #include <cmath>
 #include <string>
+#include <vector>
 
 #include "../../include/clef_hip.h"
 #include "common.hpp"
+#include "ragged.hpp"
 #include "scan.hpp"
 
 namespace clef {
@@ -32,7 +34,7 @@ using clef::fail;
 
 extern "C" const char* clef_hip_last_error(void) { return clef::g_last_error.c_str(); }
 
-extern "C" int clef_hip_abi_version(void) { return 1; }
+extern "C" int clef_hip_abi_version(void) { return 2; }
 
 static bool valid_dtype(int d) { return d == CLEF_F32 || d == CLEF_F16; }
 
@@ -196,4 +198,35 @@ extern "C" int clef_delta_scan_conv(const void* mixed, int64_t ld_mixed, int dty
   p.conv_channels = W;
   clef::scan_carve_workspace(p, workspace, precision);
   return clef::scan_launch(p, precision, static_cast<hipStream_t>(stream));
+}
+
+// The ragged launch tables on the host, by the device kernels' own steps
+// (ragged.hpp) run for every thread index in turn.
+extern "C" int clef_ragged_plan(const int32_t* cu_seqlens, int nseq, int T, int unit, int32_t* spans,
+                                int32_t* table, size_t table_entries) {
+  using namespace clef;
+  CLEF_REQUIRE(cu_seqlens && spans, "ragged plan: null pointer");
+  CLEF_REQUIRE(nseq >= 1 && nseq <= kMaxRaggedSeq && T >= 1 && T <= (1 << 20), "ragged plan: 1..4096 sequences");
+  CLEF_REQUIRE(unit == 64 || unit == 128, "ragged plan: unit 64 (scan chunks) or 128 (attention query tiles)");
+  const size_t cap = (size_t)(T + unit - 1) / unit + nseq;
+  CLEF_REQUIRE(!table || table_entries >= cap, "ragged plan: table smaller than ceil(T / unit) + nseq entries");
+  std::vector<int> part(kTabThreads), R(nseq + 1), stab(4 * (size_t)nseq), ctab(2 * cap), keys(cap);
+  const Ragged g{cu_seqlens, nseq, T, part.data(), R.data()};
+  int total = 0;
+  for (int t = 0; t < kTabThreads; ++t) rg_spans_1(g, t);
+  for (int t = 0; t < kTabThreads; ++t) rg_spans_2(g, t);
+  for (int t = 0; t < kTabThreads; ++t) rg_spans_3(g, t);
+  for (int t = 0; t < kTabThreads; ++t) rg_count_4(g, t, unit);
+  for (int t = 0; t < kTabThreads; ++t) rg_count_5(g, t, &total);
+  if ((size_t)total > cap) return fail(-3, "ragged plan: the tables exceed their capacity");
+  if (unit == 64) {
+    for (int t = 0; t < kTabThreads; ++t) rg_scan_6(g, t, unit, ctab.data(), stab.data());
+  } else {
+    for (int t = 0; t < kTabThreads; ++t) rg_attn_6(g, t, unit, 0, keys.data());
+    for (int t = 0; t < kTabThreads; ++t) rg_attn_7(g, t, unit, total, keys.data(), ctab.data());
+  }
+  for (int j = 0; j <= nseq; ++j) spans[j] = R[j];
+  if (table)
+    for (int i = 0; i < 2 * total; ++i) table[i] = ctab[i];
+  return total;
 }

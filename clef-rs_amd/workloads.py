@@ -145,3 +145,16 @@ def block_flops_per_token(config, T):
         else:
             f += 2 * H * (2 * key + 2 * value + 2 * Hv) + 2 * value * H
     return f
+
+
+def ragged_workload(config, seed=4, requests=32, lo=128, hi=4096, prefix=512):
+    """Ragged batch: `requests` lengths uniform in [lo, hi], one shared prefix
+    of `prefix` token ids and the packed request ids (numpy, seeded).
+    Returns (prefix_ids, lens, packed_ids, cu_seqlens)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, requests)
+    prefix_ids = rng.integers(0, config["vocab_size"], prefix)
+    packed = rng.integers(0, config["vocab_size"], int(lens.sum()))
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    return prefix_ids, lens, packed, cu

@@ -69,7 +69,8 @@ int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, in
  * Ragged batch of nseq independent sequences packed along the token axis
  * (T tokens in total; sequence s is tokens cu_seqlens[s] .. cu_seqlens[s+1]-1,
  * cu_seqlens a device int32 array of nseq + 1 non-decreasing offsets in
- * [0, T]).  Each sequence runs the recurrence above from its own initial
+ * [0, T]; see clef_ragged_plan for other tables).  Each sequence runs the
+ * recurrence above from its own initial
  * state: initial + s * initial_stride floats ([Hv, dk, dv] f32; stride 0 =
  * one state shared by all, NULL = zero states); final_states, if not NULL,
  * receives [nseq, Hv, dk, dv].  Layouts, dtypes and limits as above, with
@@ -79,6 +80,22 @@ int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, in
  */
 size_t clef_delta_scan_varlen_workspace(int T, int nseq, int Hk, int Hv, int dk, int dv, int chunk,
                                         int precision);
+/*
+ * Ragged batches and malformed offsets: every entry point that takes
+ * cu_seqlens first makes the offsets monotone, R[j] = max over i <= j of
+ * cu_seqlens[i] clamped to [0, T], and sequence s is then tokens R[s] ..
+ * R[s+1]-1 (R equals cu_seqlens for a valid table).  So an offset table the
+ * host cannot inspect (it is device memory) never takes a kernel outside its
+ * buffers.  clef_ragged_plan evaluates the same tables on the host, with the
+ * device kernels' code: cu_seqlens in host memory; unit 64 (the scan's
+ * chunks) or 128 (attention's query tiles); spans receives R ([nseq + 1]);
+ * table, if not NULL, receives the units (scan: {first token, tokens} per
+ * chunk; attention: {sequence, tile} in launch order), table_entries >=
+ * ceil(T / unit) + nseq.  Returns the unit count (at most that bound) or < 0.
+ * No counterpart in the reference (one request per call there).
+ */
+int clef_ragged_plan(const int32_t* cu_seqlens, int nseq, int T, int unit, int32_t* spans, int32_t* table,
+                     size_t table_entries);
 int clef_delta_scan_varlen(const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
                            int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
                            const int32_t* cu_seqlens, int nseq, int T, int Hk, int Hv, int dk, int dv,
@@ -146,14 +163,17 @@ int clef_gemm_swiglu(const void* x, int64_t ldx, const void* wg, const void* wu,
  * consecutive bytes straight into registers, leaving the LDS to the
  * activations.  K must be a multiple of 64.  clef_gemm_packed: as clef_gemm,
  * epilogues CLEF_EPI_STORE and CLEF_EPI_RESIDUAL with the same roundings
- * (SwiGLU: clef_gemm_swiglu).  Extends the reference's GemmKernel
+ * (SwiGLU: clef_gemm_swiglu); packed_bytes is the size of the packed buffer
+ * and must equal clef_gemm_pack_bytes(N, K), so every weight read stays
+ * inside the buffer (a buffer of another size is rejected before launch).
+ * Extends the reference's GemmKernel
  * (neural.rs:50-58), whose weights stay row-major; clef_gemm remains the
  * drop-in entry point.
  */
 size_t clef_gemm_pack_bytes(int N, int K);
 int clef_gemm_pack(const void* w, int64_t ldw, int N, int K, int dtype, void* packed, void* stream);
-int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, void* y, int64_t ldy, int M, int N, int K,
-                     int dtype_in, int dtype_out, int epilogue, void* stream);
+int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, size_t packed_bytes, void* y, int64_t ldy,
+                     int M, int N, int K, int dtype_in, int dtype_out, int epilogue, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Pointwise pieces around the scan                                        */
@@ -367,28 +387,55 @@ size_t clef_backbone_workspace(const clef_backbone* b, int T, int prefix_tokens)
 size_t clef_backbone_prefix_bytes(const clef_backbone* b, int tokens);
 /*
  * ids: host int32 [T], each < vocab.  initial: a prefix state buffer written
- * by an earlier capture (initial_tokens of them), or NULL.  capture in 1..T-1
- * writes the state after `capture` tokens into `saved` (which must hold
- * clef_backbone_prefix_bytes(b, capture) bytes); initial and capture are
- * exclusive (qwen.rs:345-359).  hidden: f32 [(initial_tokens + T), H], the
- * final-normed hidden states, prefix rows included.
+ * by an earlier capture (initial_tokens of them), or NULL; initial_bytes is
+ * its size and must equal clef_backbone_prefix_bytes(b, initial_tokens), so a
+ * state captured by a backbone of another shape (the reference's layer-count
+ * check, qwen.rs:355) or passed with the wrong token count is rejected before
+ * any launch.  capture in 1..T-1 writes the state after `capture` tokens into
+ * `saved` (saved_bytes >= clef_backbone_prefix_bytes(b, capture)); initial
+ * and capture are exclusive (qwen.rs:345-359).  hidden: f32
+ * [(initial_tokens + T), H], the final-normed hidden states, prefix rows
+ * included.
  */
 int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T, const void* initial,
-                          int initial_tokens, int capture, void* saved, float* hidden,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          int initial_tokens, size_t initial_bytes, int capture, void* saved,
+                          size_t saved_bytes, float* hidden, void* workspace, size_t workspace_bytes,
+                          void* stream);
 /*
  * Ragged batch of requests resumed from one shared prefix state (a prefix
  * cache hit for each, prefix_cache.rs:135-177): ids is the host int32 packed
  * token stream, cu_seqlens the host int32 offsets (cu_seqlens[0] = 0, each
  * sequence 1..max_tokens - initial_tokens long, at most 4096 sequences and
- * 2^20 tokens).  hidden: f32 [T, H], the final-normed hidden states of the
- * packed tokens; sequence s's rows equal clef_backbone_prefill of its ids
- * from `initial`.  No counterpart in the reference (one request per call).
+ * 2^20 tokens; initial_bytes as for clef_backbone_prefill).  hidden: f32
+ * [T, H], the final-normed hidden states of the packed tokens; sequence s's
+ * rows equal clef_backbone_prefill of its ids from `initial`.  No
+ * counterpart in the reference (one request per call).
  */
 size_t clef_backbone_varlen_workspace(const clef_backbone* b, int T, int nseq, int prefix_tokens);
 int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids, const int32_t* cu_seqlens, int nseq,
-                                 const void* initial, int initial_tokens, float* hidden, void* workspace,
-                                 size_t workspace_bytes, void* stream);
+                                 const void* initial, int initial_tokens, size_t initial_bytes, float* hidden,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Cooperative cancellation and deadline, the reference's Control
+ * (crates/core/src/models/mod.rs:45-59), checked where the reference checks
+ * it: when a prefill starts (qwen.rs:344) and before each layer (qwen.rs:380).
+ * `cancel` points to a host flag that another thread may set (nonzero =
+ * cancel; NULL = never); `deadline` is an absolute time in seconds on the
+ * clock of clef_monotonic_seconds() (0 = none).  A check that fails returns
+ * CLEF_CANCELLED or CLEF_DEADLINE_EXCEEDED (Error::Cancelled /
+ * Error::DeadlineExceeded) and launches nothing more; launches already
+ * enqueued on the stream still run, and the outputs of a prefill that
+ * returned an error are unspecified.  control NULL clears it.  The control
+ * is read at every check, so the flag must outlive the prefills it governs.
+ */
+enum { CLEF_CANCELLED = -20, CLEF_DEADLINE_EXCEEDED = -21 };
+typedef struct {
+    const volatile int32_t* cancel;
+    double deadline;
+} clef_control;
+int clef_backbone_set_control(clef_backbone* b, const clef_control* control);
+double clef_monotonic_seconds(void);
 
 /*
  * Diagnostics, the counterpart of the reference's test-only `measured!`

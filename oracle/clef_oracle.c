@@ -366,9 +366,25 @@ void oracle_rms(const float* x, int rows, int width, const float* w, float eps, 
     }
 }
 
+/* Exact-accumulation mode (oracle_set_exact_dots): projection dot products
+ * accumulated in f64 and rounded to f32 once.  Not the reference's arithmetic
+ * (Candle's f32 GEMM): a yardstick closer to the exact result, against which
+ * the f32 restatement and the device path can both be measured. */
+static int g_exact_dots = 0;
+void oracle_set_exact_dots(int on) { g_exact_dots = on != 0; }
+
 /* y = x W^T.  Eight interleaved partial sums per dot product (a fixed order,
  * so the result does not depend on the thread count). */
 static float dot8(const float* a, const float* b, int K) {
+    if (g_exact_dots) {
+        double d[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int i = 0;
+        for (; i + 8 <= K; i += 8)
+            for (int l = 0; l < 8; ++l) d[l] += (double)a[i + l] * (double)b[i + l];
+        double s = ((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7]));
+        for (; i < K; ++i) s += (double)a[i] * (double)b[i];
+        return (float)s;
+    }
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int i = 0;
     for (; i + 8 <= K; i += 8)

@@ -132,6 +132,8 @@ int oracle_backbone_prefill(const oracle_backbone* b, const int* ids, int T,
 
 /* Threads used by the OpenMP regions (0 = runtime default). */
 void oracle_set_threads(int n);
+/* f64-accumulated projection dot products (a yardstick, not the reference's arithmetic). */
+void oracle_set_exact_dots(int on);
 int oracle_get_threads(void);
 
 #ifdef __cplusplus

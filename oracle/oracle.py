@@ -76,6 +76,7 @@ def _declare(L):
                                           C.c_void_p, i, C.c_void_p, _f32p]
     L.oracle_backbone_prefill.restype = i
     L.oracle_set_threads.argtypes = [i]
+    L.oracle_set_exact_dots.argtypes = [i]
     L.oracle_get_threads.restype = i
     L.oracle_f32_to_f16.argtypes = [C.c_float]
     L.oracle_f32_to_f16.restype = C.c_uint16
@@ -97,6 +98,18 @@ def _ptr(a):
 
 def set_threads(n: int):
     lib().oracle_set_threads(int(n))
+
+
+class exact_dots:
+    """Context in which the oracle accumulates its projection dot products
+    in f64 (rounded to f32 once): a yardstick nearer the exact result."""
+
+    def __enter__(self):
+        lib().oracle_set_exact_dots(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().oracle_set_exact_dots(0)
 
 
 def threads() -> int:

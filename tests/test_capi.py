@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(clef):
 
 
 def test_abi_version(clef):
-    assert clef.lib().clef_hip_abi_version() == 1
+    assert clef.lib().clef_hip_abi_version() == 2
 
 
 @pytest.mark.parametrize("shape", [(0, 32, 32, 128, 128), (4097 * 256, 16, 32, 128, 128),
@@ -82,3 +82,68 @@ def test_backbone_create_rejects_bad_config(clef):
     handle = C.c_void_p()
     assert clef.lib().clef_backbone_create(C.byref(cfg), layers, 1, 1, C.byref(handle)) < 0
     assert not handle.value
+
+
+def _check_plan(clef, cu, T, unit):
+    """The host evaluation of the ragged tables (the device kernels' code):
+    monotone spans inside [0, T], units tiling each span, and never more
+    units than the ceil(T / unit) + nseq the workspaces reserve."""
+    import numpy as np
+    cu = np.asarray(cu, np.int64)
+    nseq = len(cu) - 1
+    spans, units = clef.ragged_plan(cu, T, unit)
+    assert spans[0] >= 0 and spans[-1] <= T and (np.diff(spans) >= 0).all()
+    # the spans are the running maximum of the clamped offsets
+    assert (spans == np.maximum.accumulate(np.clip(cu, 0, T))).all()
+    assert len(units) <= (T + unit - 1) // unit + nseq
+    lens = np.diff(spans)
+    assert len(units) == int(((lens + unit - 1) // unit).sum())
+    if unit == 64:
+        covered = np.zeros(T, np.int64)
+        for t0, n in units:
+            assert 0 <= t0 and 1 <= n <= 64 and t0 + n <= T
+            covered[t0:t0 + n] += 1
+        inside = np.zeros(T, np.int64)
+        for s in range(nseq):
+            inside[spans[s]:spans[s + 1]] += 1
+        assert (covered == inside).all()  # each token of a span in exactly one chunk
+    else:
+        seen = set()
+        for s, t in units:
+            assert 0 <= s < nseq and 0 <= t and t * 128 < lens[s]
+            seen.add((int(s), int(t)))
+        assert len(seen) == len(units)
+    return spans
+
+
+@pytest.mark.parametrize("unit", [64, 128])
+def test_ragged_plan_valid_table_is_unchanged(clef, unit):
+    import numpy as np
+    rng = np.random.default_rng(4)
+    lens = rng.integers(1, 700, 37)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    spans = _check_plan(clef, cu, int(cu[-1]), unit)
+    assert (spans == cu).all()
+
+
+@pytest.mark.parametrize("unit", [64, 128])
+@pytest.mark.parametrize("cu,T", [
+    ([0, 1000, 0, 1000, 0, 1000], 1000),          # overlapping sequences
+    ([0, 5000, 6000], 1000),                      # offsets past T
+    ([-50, 100, 40, 900, 300, 1000], 1000),       # negative and non-monotone
+    ([0] * 4096 + [4096], 4096),                  # many empty sequences
+    ([0, 4096] * 2048 + [4096], 4096),            # 4096 sequences, all overlapping
+    ([2 ** 31 - 1, -(2 ** 31), 7, 3], 10),        # extreme values
+])
+def test_ragged_plan_malformed_tables_stay_in_bounds(clef, unit, cu, T):
+    _check_plan(clef, cu, T, unit)
+
+
+def test_ragged_plan_rejects_bad_arguments(clef):
+    import numpy as np
+    cu = np.array([0, 10], np.int32)
+    sp = np.zeros(2, np.int32)
+    L = clef.lib()
+    assert L.clef_ragged_plan(cu.ctypes.data, 1, 10, 32, sp.ctypes.data, None, 0) < 0
+    assert L.clef_ragged_plan(cu.ctypes.data, 0, 10, 64, sp.ctypes.data, None, 0) < 0
+    assert L.clef_ragged_plan(cu.ctypes.data, 1, 10, 64, sp.ctypes.data, sp.ctypes.data, 1) < 0

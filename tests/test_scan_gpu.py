@@ -2,10 +2,15 @@
 
 Bars: strict f32 profile rtol 1e-4 / atol 1e-5 against the CPU
 F32 recurrence (qwen.rs:826-882); mixed f16-MFMA profile rtol 2e-2 with an
-absolute floor of 2e-2 * max|expected| (elementwise relative error is
-meaningless at near-zero outputs).  Capture/resume at chunk-aligned
-boundaries must be bit-exact (metal.rs:819-868 contract).
+absolute floor of 1e-2 * RMS(expected) (the f16 operands perturb every
+output by a fraction of the outputs' typical size, so elements near zero
+need a floor).  Capture/resume at chunk-aligned boundaries must be
+bit-exact (metal.rs:819-868 contract).  Achieved errors are appended to the
+JSON file named by CLEF_PARITY_LOG.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -27,11 +32,26 @@ def _close(actual, expected, rtol, atol):
                            f" at {np.unravel_index(err.argmax(), err.shape)}")
 
 
-def _check(actual, expected, precision):
+def _record(name, actual, expected):
+    path = os.environ.get("CLEF_PARITY_LOG")
+    if path:
+        a, e = np.asarray(actual, np.float64), np.asarray(expected, np.float64)
+        err = np.abs(a - e)
+        rms = float(np.sqrt(np.mean(e * e)))
+        with open(path, "a") as f:
+            f.write(json.dumps({"test": name, "max_abs": float(err.max()),
+                                "max_abs_over_rms": float(err.max() / max(rms, 1e-30)),
+                                "frac_outside_rtol_2e-2": float((err > 2e-2 * np.abs(e)).mean())}) + "\n")
+
+
+def _check(actual, expected, precision, name=None):
+    if name:
+        _record(name, actual, expected)
     if precision == "strict":
         _close(actual, expected, STRICT_RTOL, STRICT_ATOL)
     else:
-        _close(actual, expected, MIXED_RTOL, MIXED_RTOL * np.abs(expected).max())
+        e = np.asarray(expected, np.float64)
+        _close(actual, expected, MIXED_RTOL, 1e-2 * np.sqrt(np.mean(e * e)))
 
 
 def case_inputs(seed, T, Hk, Hv, dk, dv, dtype=torch.float32, device="cuda"):
@@ -57,8 +77,8 @@ def test_scan_small_config_seed0(clef, precision):
     q, k, v, g, beta = case_inputs(0, 256, 4, 4, 64, 64)
     out, _, final = clef.DeltaScan(64, 64, precision).prefill(q, k, v, g, beta)
     eo, _, ef = oracle.delta_scan(*_np(q, k, v, g, beta))
-    _check(out.cpu().numpy(), eo, precision)
-    _check(final.cpu().numpy(), ef, precision)
+    _check(out.cpu().numpy(), eo, precision, f"scan T=256 H=4 64/64 {precision}: out")
+    _check(final.cpu().numpy(), ef, precision, f"scan T=256 H=4 64/64 {precision}: final state")
 
 
 @gpu
@@ -164,8 +184,8 @@ def test_scan_full_layer_config(clef, precision):
     q, k, v, g, beta = case_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16)
     out, _, final = clef.DeltaScan(128, 128, precision).prefill(q, k, v, g, beta)
     eo, _, ef = oracle.delta_scan(*_np(q, k, v, g, beta))
-    _check(out.cpu().numpy(), eo, precision)
-    _check(final.cpu().numpy(), ef, precision)
+    _check(out.cpu().numpy(), eo, precision, f"scan T=4096 16/32 128/128 {precision}: out")
+    _check(final.cpu().numpy(), ef, precision, f"scan T=4096 16/32 128/128 {precision}: final state")
 
 
 @gpu
