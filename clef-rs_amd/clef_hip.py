@@ -47,6 +47,8 @@ SIGNATURES = {
     "clef_delta_scan_workspace": (_z, [_i] * 7),
     "clef_delta_scan": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _i, _i, _i,
                              _p, _i, _p, _l, _i, _p, _p, _p, _z, _p]),
+    "clef_delta_scan_noalloc": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _i, _i, _i, _i, _i, _i, _i,
+                                     _p, _i, _p, _l, _i, _p, _p, _p]),
     "clef_delta_scan_varlen_workspace": (_z, [_i] * 8),
     "clef_ragged_plan": (_i, [_p, _i, _i, _i, _p, _p, _z]),
     "clef_delta_scan_varlen": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i,

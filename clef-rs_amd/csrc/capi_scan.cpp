@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -111,6 +112,59 @@ extern "C" int clef_delta_scan(const void* q, const void* k, const void* v, int6
   p.captured = captured; p.final_state = final_state;
   clef::scan_carve_workspace(p, workspace, precision);
   return clef::scan_launch(p, precision, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// clef_delta_scan_noalloc: the scan's workspace in a file-scope device array
+// (one copy per GPU, held until the process ends).  Host code never passes
+// `scratch` itself to a kernel or a copy: its name is a host-side stand-in.
+// The device address of each GPU's copy comes from hipGetSymbolAddress, once
+// per device with that device current, and only that address is used.
+namespace {
+
+__device__ __attribute__((aligned(256))) unsigned char scratch[CLEF_SCAN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(static_cast<int>(e), std::string("scan scratch: hipGetDevice: ") + hipGetErrorString(e));
+  CLEF_REQUIRE(dev >= 0 && dev < kMaxDevices, "scan scratch: device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(e != hipSuccess ? static_cast<int>(e) : -2,
+                  std::string("scan scratch: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int clef_delta_scan_noalloc(const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
+                                       int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
+                                       int T, int Hk, int Hv, int dk, int dv, int chunk, int precision,
+                                       const float* initial, int capture, void* out, int64_t so, int dtype_out,
+                                       float* captured, float* final_state, void* stream) {
+  if (int rc = scan_dims(T, Hk, Hv, dk, dv, chunk, precision)) return rc;
+  const size_t need = clef::scan_workspace_bytes(T, Hk, Hv, dk, precision);
+  CLEF_REQUIRE(need <= CLEF_SCAN_SCRATCH_BYTES,
+               "DeltaNet scan (no-alloc): the workspace this shape needs exceeds the "
+               "CLEF_SCAN_SCRATCH_BYTES scratch array");
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  // every scratch byte the kernels read is written earlier in the same call,
+  // so nothing left by an earlier call needs clearing
+  return clef_delta_scan(q, k, v, sqk, sv, dtype_qkv, g, beta, sgb, dtype_gb, T, Hk, Hv, dk, dv, chunk, precision,
+                         initial, capture, out, so, dtype_out, captured, final_state, ws, CLEF_SCAN_SCRATCH_BYTES,
+                         stream);
 }
 
 extern "C" size_t clef_delta_scan_varlen_workspace(int T, int nseq, int Hk, int Hv, int dk, int dv, int chunk,

@@ -66,6 +66,27 @@ int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, in
                     void* stream);
 
 /*
+ * clef_delta_scan without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * scan's scratch is a file-scope device array of CLEF_SCAN_SCRATCH_BYTES
+ * (96 MiB) in this library, one per GPU, held until the process ends (its
+ * address is looked up once per device, at the first call with that device
+ * current; the stream must belong to the current device).  A shape whose
+ * clef_delta_scan_workspace exceeds it is rejected before any launch (the
+ * full layer shape T = 4096, Hk = 16, Hv = 32, dk = dv = 128 needs 82.5 MiB in
+ * the mixed profile).  Arguments and results as clef_delta_scan.  Every call
+ * on a GPU uses that GPU's one array: calls that overlap in time on one GPU
+ * (other streams, other threads) race, and the caller must serialize them.
+ */
+#define CLEF_SCAN_SCRATCH_BYTES ((size_t)96 << 20)
+int clef_delta_scan_noalloc(const void* q, const void* k, const void* v, int64_t sqk, int64_t sv,
+                            int dtype_qkv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
+                            int T, int Hk, int Hv, int dk, int dv, int chunk, int precision,
+                            const float* initial, int capture, void* out, int64_t so, int dtype_out,
+                            float* captured, float* final_state, void* stream);
+
+/*
  * Ragged batch of nseq independent sequences packed along the token axis
  * (T tokens in total; sequence s is tokens cu_seqlens[s] .. cu_seqlens[s+1]-1,
  * cu_seqlens a device int32 array of nseq + 1 non-decreasing offsets in
