@@ -11,8 +11,10 @@ with f32 state).  Inputs and weights are resident in HBM before timing.
 The JSON line reports whole-prefill tokens/s, the projection GEMMs' TFLOP/s
 and the scan's fraction of the HBM roofline (both from HIP events recorded on
 the prefill's stream around each launch), the stand-alone scan of the full
-layer shape (T=4096, Hk=16, Hv=32, 128/128, f16 in, f32 out) and the CPU
-oracle's throughput on a bounded sample of the same workload.
+layer shape (T=4096, Hk=16, Hv=32, 128/128, f16 in, f32 out) in both
+precision profiles, the projection GEMMs at the 2048 x 2048 shapes in f16 and
+f32, the same block in the f32 profile, and the CPU oracle on bounded
+samples of the same workloads.
 """
 from __future__ import annotations
 
@@ -39,7 +41,10 @@ def parse():
     ap.add_argument("--profile", choices=("mixed", "f32"), default="mixed")
     ap.add_argument("--cpu-tokens", type=int, default=2048,
                     help="tokens of the bounded CPU-oracle sample (0 disables it)")
-    ap.add_argument("--cpu-runs", type=int, default=4)
+    ap.add_argument("--cpu-runs", type=int, default=3, help="timed CPU runs (median) after one warm-up")
+    ap.add_argument("--sweep", type=int, default=1,
+                    help="also time the 2048 x 2048 projection GEMMs (f16 and f32), the stand-alone scan in "
+                         "both profiles and the block in the f32 profile (0: skip)")
     ap.add_argument("--ragged", type=int, default=1,
                     help="also time the ragged batch: 32 requests of U[128, 4096] tokens behind one shared "
                          "512-token prefix (0: skip)")
@@ -51,15 +56,17 @@ def parse():
 
 def measured_traffic(T, profile):
     """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy of known size), or
-    None when no summary matches this workload."""
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy of known size) and
+    that summary's path, or (None, None) when no summary matches this
+    workload.  Counters need a profiler run of their own, so this is the
+    committed measurement of the same workload, not one taken in this run."""
     path = ROOT / "profiles" / f"gemm_traffic_T{T}_{profile}.md"
     if not path.exists():
-        return None
+        return None, None
     for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch"):
-            return int(float(line.split("=")[1]))
-    return None
+            return int(float(line.split("=")[1])), str(path.relative_to(ROOT))
+    return None, None
 
 
 def event_ms(fn, steps, warmup, torch):
@@ -92,16 +99,91 @@ def cpu_baseline(cfg, weights, ids, tokens, runs):
     host = {k: v.float().cpu().numpy() for k, v in weights.items() if k != emb_name}
     host[emb_name] = weights[emb_name][torch.from_numpy(uniq).long().to(weights[emb_name].device)].float().cpu().numpy()
     b = oracle.Backbone(dict(cfg, vocab_size=len(uniq)), host)
-    b.prefill(inv[:16].astype(np.int32))  # touch pages
+    med, total = _median_after_warmup(lambda: b.prefill(inv.astype(np.int32)), runs)
+    out = {"value": round(tokens / med, 2), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+           "sample": f"oracle F32 prefill of the first {tokens} tokens of the same block workload "
+                     f"(same weights), median of {runs} runs after one warm-up ({total:.1f} s in all)"}
+    out["ops"] = cpu_ops(runs)
+    return out
+
+
+def _median_after_warmup(fn, runs):
+    t_all = time.perf_counter()
+    fn()
     times = []
     for _ in range(runs):
         t0 = time.perf_counter()
-        b.prefill(inv.astype(np.int32))
+        fn()
         times.append(time.perf_counter() - t0)
-    best = min(times)
-    return {"value": round(tokens / best, 2), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
-            "sample": f"oracle F32 prefill of the first {tokens} tokens of the same block workload "
-                      f"(same weights), best of {runs} runs ({sum(times):.1f} s total)"}
+    return sorted(times)[len(times) // 2], time.perf_counter() - t_all
+
+
+def cpu_ops(runs):
+    """The oracle's scan at the small (T=256, H=4, 64/64) and full layer
+    shapes and one 2048 x 2048 x 8192 projection, beside the GPU figures."""
+    import numpy as np
+    import torch
+
+    import oracle  # CPU baseline leg only
+    import workloads
+
+    res = {}
+    for name, shape in (("scan_T256_H4_64", workloads.SCAN_SMALL), ("scan_T4096_16x32_128", workloads.SCAN_LAYER)):
+        q, k, v, g, beta = (x.numpy() for x in workloads.scan_inputs(**shape, device="cpu"))
+        n = 1 if shape["T"] > 1024 else runs
+        med, _ = _median_after_warmup(lambda: oracle.delta_scan(q, k, v, g, beta), n)
+        res[name + "_ms"] = round(med * 1e3, 2)
+    x, w = (t.float().numpy() for t in workloads.gemm_inputs(1, 2048, 8192, 2048, dtype=torch.float32,
+                                                              device="cpu"))
+    med, _ = _median_after_warmup(lambda: oracle.linear(x, w), runs)
+    res["gemm_2048x8192x2048_ms"] = round(med * 1e3, 2)
+    res["gemm_2048x8192x2048_tfs"] = round(2 * 2048 * 8192 * 2048 / med / 1e12, 4)
+    return res
+
+
+def gemm_sweep(clef_hip, workloads, torch, dev, steps, warmup):
+    """The projection GEMMs at M = K = 2048 (N = 8192 fused in-projection,
+    2048 out-projection, 6144 SwiGLU gate + up), x ~ N(0,1), W ~ N(0,0.02),
+    seed 1, f16 and f32 operands, f32 accumulation; HIP events on the
+    launching stream, outputs preallocated."""
+    rows = []
+    for dt, name in ((torch.float16, "f16"), (torch.float32, "f32")):
+        peak = MFMA_PEAK_TFS[name]
+        for label, N in (("in_proj", 8192), ("out_proj", 2048), ("swiglu", 6144)):
+            x, w = workloads.gemm_inputs(1, 2048, N, 2048, dtype=dt, device=dev)
+            y = torch.empty((2048, N), dtype=dt, device=dev)
+            if label == "swiglu":
+                _, wu = workloads.gemm_inputs(2, 2048, N, 2048, dtype=dt, device=dev)
+                fn = lambda: clef_hip.gemm_swiglu(x, w, wu, out=y)
+                flops = 4.0 * 2048 * N * 2048
+            else:
+                fn = lambda: clef_hip.gemm(x, w, out=y)
+                flops = 2.0 * 2048 * N * 2048
+            ms = event_ms(fn, steps, warmup, torch)
+            tfs = flops / (ms * 1e-3) / 1e12
+            rows.append({"dtype": name, "shape": f"2048x{N}x2048" + (" x2 (gate+up)" if label == "swiglu" else ""),
+                         "op": label, "us": round(ms * 1e3, 2), "tflops": round(tfs, 2), "frac": round(tfs / peak, 4)})
+    return rows
+
+
+def scan_standalone(clef_hip, workloads, torch, dev, steps, warmup):
+    """The full-layer scan (T=4096, Hk=16, Hv=32, 128/128, seed 2; f16 q/k/v/g/beta,
+    f32 state and output) in the mixed (f16 MFMA) and strict (f32 MFMA) profiles."""
+    q, k, v, gg, beta = workloads.scan_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16, device=dev)
+    sout = torch.empty((4096, 32, 128), device=dev)
+    sbytes = workloads.scan_bytes(4096, 16, 32, 128, 128, 2, 4)
+    sflops = workloads.scan_flops(4096, 16, 32, 128, 128)
+    out = {}
+    for prec, peak_name in (("mixed", "f16"), ("strict", "f32")):
+        scan = clef_hip.DeltaScan(128, 128, prec)
+        sms = event_ms(lambda: scan.prefill(q, k, v, gg, beta, out=sout, want_final=True), steps, warmup, torch)
+        gbs = sbytes / (sms * 1e-3) / 1e9
+        out[prec] = {"us": round(sms * 1e3, 2), "GBs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                     "tflops": round(sflops / (sms * 1e-3) / 1e12, 2),
+                     "frac_mfma": round(sflops / (sms * 1e-3) / 1e12 / MFMA_PEAK_TFS[peak_name], 4)}
+    out["algorithmic_bytes"] = sbytes
+    out["algorithmic_flops"] = sflops
+    return out
 
 
 def ragged_batch(model, cfg, args, torch, np, dev):
@@ -172,13 +254,9 @@ def main():
     scan_gbs = sc["bytes"] / (sc["ms"] * 1e-3) / 1e9
 
     # ---- stand-alone scan at the full layer shape (f16 in, f32 state and out)
-    q, k, v, gg, beta = workloads.scan_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16, device=dev)
-    scan = clef_hip.DeltaScan(128, 128, "mixed" if args.profile == "mixed" else "strict")
-    sout = torch.empty((4096, 32, 128), device=dev)
-    sfinal = torch.empty((32, 128, 128), device=dev)
-    sms = event_ms(lambda: scan.prefill(q, k, v, gg, beta, out=sout, want_final=True), args.steps, args.warmup, torch)
-    sbytes = workloads.scan_bytes(4096, 16, 32, 128, 128, 2, 4)
-    del sfinal
+    scans = scan_standalone(clef_hip, workloads, torch, dev, args.steps, args.warmup)
+    sprof = scans["mixed" if args.profile == "mixed" else "strict"]
+    traffic, traffic_src = measured_traffic(T, args.profile)
 
     line = {
         "metric": "prefill tok/s (hybrid block, T=4096); GEMM TFLOP/s + scan % of HBM roofline",
@@ -205,7 +283,8 @@ def main():
             "peak": MFMA_PEAK_TFS[dt],
             "unit": "TFLOP/s",
             "frac": round(gemm_tfs / MFMA_PEAK_TFS[dt], 4),
-            "traffic": measured_traffic(T, args.profile),
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             # per launch (event-timed on the backbone's stream), to set beside
             # the kernel-trace averages
             "launches_per_step": int(g["launches"]),
@@ -215,16 +294,27 @@ def main():
         "scan": {
             "in_block_GBs": round(scan_gbs, 1),
             "in_block_frac_hbm": round(scan_gbs / HBM_PEAK_GBS, 4),
-            "layer_shape_us": round(sms * 1e3, 2),
-            "layer_shape_GBs": round(sbytes / (sms * 1e-3) / 1e9, 1),
-            "layer_shape_frac_hbm": round(sbytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": sbytes,
+            "layer_shape_us": sprof["us"],
+            "layer_shape_GBs": sprof["GBs"],
+            "layer_shape_frac_hbm": sprof["frac_hbm"],
+            "algorithmic_bytes": scans["algorithmic_bytes"],
+            "layer_shape_by_profile": {k: v for k, v in scans.items() if k in ("mixed", "strict")},
         },
         "breakdown_ms_per_step": {k: round(v["ms"], 4) for k, v in per_step.items()},
         "launches_per_step": {k: int(v["launches"]) for k, v in per_step.items()},
     }
     if args.ragged:
         line["ragged"] = ragged_batch(model, cfg, args, torch, np, dev)
+    if args.sweep:
+        line["gemm_2048"] = gemm_sweep(clef_hip, workloads, torch, dev, args.steps, args.warmup)
+        if args.profile == "mixed":
+            del model
+            torch.cuda.empty_cache()
+            m32 = clef_hip.Backbone(cfg, weights, profile="f32", max_tokens=max(8192, T))
+            ms32 = event_ms(lambda: m32.prefill(ids, hidden=hidden), max(2, args.steps // 3), 1, torch)
+            line["f32_profile"] = {"tok_s": round(T / (ms32 / 1e3), 1), "ms_per_step": round(ms32, 3),
+                                   "steps": max(2, args.steps // 3)}
+            del m32
     if args.cpu_tokens > 0:
         line["cpu_baseline"] = cpu_baseline(cfg, weights, ids, min(args.cpu_tokens, T), args.cpu_runs)
     print(json.dumps(line), flush=True)
