@@ -53,8 +53,6 @@ SIGNATURES = {
     "clef_ragged_plan": (_i, [_p, _i, _i, _i, _p, _p, _z]),
     "clef_delta_scan_varlen": (_i, [_p, _p, _p, _l, _l, _i, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i,
                                     _p, _l, _p, _l, _i, _p, _p, _z, _p]),
-    "clef_delta_scan_conv": (_i, [_p, _l, _i, _p, _i, _p, _i, _l, _p, _p, _p, _l, _i, _p, _i, _i, _i, _i, _i, _i,
-                                  _i, _i, _p, _l, _i, _p, _l, _i, _p, _p, _p, _z, _p]),
     "clef_silu_mul": (_i, [_p, _p, _p, _l, _i, _p]),
     "clef_gemm": (_i, [_p, _l, _p, _l, _p, _l, _i, _i, _i, _i, _i, _i, _p]),
     "clef_gemm_swiglu": (_i, [_p, _l, _p, _p, _l, _p, _l, _i, _i, _i, _i, _p]),
@@ -234,52 +232,6 @@ class DeltaScan:
             _ptr(cu_seqlens), nseq, T, Hk, Hv, dk, dv, self.chunk, self.precision, _ptr(initial), stride,
             _ptr(out), so, _dt(out), _ptr(final), _ptr(ws), ws.numel(), _stream()))
         return out, final
-
-
-def delta_scan_conv(scan, mixed, Hk, Hv, conv_w, g, beta, history=None, cu_seqlens=None, initial=None,
-                    capture=0, out_dtype=torch.float32, want_final=True):
-    """The mixer's conv + SiLU folded into the scan (clef_delta_scan_conv).
-
-    mixed: [T, >= 2 Hk dk + Hv dv] raw projection rows [q | k | v | ...];
-    conv_w: f32 [2 Hk dk + Hv dv, 4]; history: f32 [rows, 2 Hk dk + Hv dv]
-    (shared by every sequence) or None; cu_seqlens: int32 device offsets or
-    None (one sequence).  Returns (out, v_conv [T, Hv, dv], captured, final).
-    """
-    T = mixed.shape[0]
-    dk, dv = scan.key_dim, scan.value_dim
-    ld = _rows(mixed, "mixed")
-    dev = mixed.device
-    if conv_w.dtype != torch.float32 or not conv_w.is_contiguous() or conv_w.shape != (2 * Hk * dk + Hv * dv, 4):
-        raise ClefError(-1, "conv weights must be contiguous f32 [2 Hk dk + Hv dv, 4]")
-    hrows = 0
-    if history is not None:
-        if history.dtype != torch.float32 or not history.is_contiguous() or history.shape[1] != conv_w.shape[0]:
-            raise ClefError(-1, "history must be contiguous f32 [rows, 2 Hk dk + Hv dv]")
-        hrows = history.shape[0]
-    vconv = torch.empty((T, Hv, dv), dtype=mixed.dtype, device=dev)
-    out = torch.empty((T, Hv, dv), dtype=out_dtype, device=dev)
-    nseq, stride = 1, 0
-    if cu_seqlens is not None:
-        nseq = cu_seqlens.numel() - 1
-        if initial is not None and initial.dim() == 4:
-            stride = Hv * dk * dv
-        n = lib().clef_delta_scan_varlen_workspace(T, nseq, Hk, Hv, dk, dv, scan.chunk, scan.precision)
-        final = torch.empty((nseq, Hv, dk, dv), dtype=torch.float32, device=dev) if want_final else None
-    else:
-        n = lib().clef_delta_scan_workspace(T, Hk, Hv, dk, dv, scan.chunk, scan.precision)
-        final = torch.empty((Hv, dk, dv), dtype=torch.float32, device=dev) if want_final else None
-    if n == 0:
-        raise ClefError(-1, last_error())
-    ws = torch.empty(n + 256, dtype=torch.uint8, device=dev)
-    off = (-ws.data_ptr()) % 256
-    ws = ws[off:off + n]
-    captured = torch.empty((Hv, dk, dv), dtype=torch.float32, device=dev) if capture else None
-    _check(lib().clef_delta_scan_conv(
-        _ptr(mixed), ld, _dt(mixed), _ptr(conv_w), 4, _ptr(history), hrows, 0, _ptr(vconv),
-        _ptr(g), _ptr(beta), g.stride(0), _dt(g), _ptr(cu_seqlens), nseq, T, Hk, Hv, dk, dv, scan.chunk,
-        scan.precision, _ptr(initial), stride, int(capture), _ptr(out), Hv * dv, _dt(out), _ptr(captured),
-        _ptr(final), _ptr(ws), ws.numel(), _stream()))
-    return out, vconv, captured, final
 
 
 def ragged_plan(cu_seqlens, T, unit):

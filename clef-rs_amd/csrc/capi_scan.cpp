@@ -194,66 +194,6 @@ extern "C" int clef_delta_scan_varlen(const void* q, const void* k, const void* 
 }
 
 // the mixer's conv + SiLU folded into the scan (see include/clef_hip.h)
-extern "C" int clef_delta_scan_conv(const void* mixed, int64_t ld_mixed, int dtype_qkv, const float* conv_w,
-                                    int taps, const float* history, int history_rows, int64_t history_stride,
-                                    void* v_conv, const void* g, const void* beta, int64_t sgb, int dtype_gb,
-                                    const int32_t* cu_seqlens, int nseq, int T, int Hk, int Hv, int dk, int dv,
-                                    int chunk, int precision, const float* initial, int64_t initial_stride,
-                                    int capture, void* out, int64_t so, int dtype_out, float* captured,
-                                    float* final_states, void* workspace, size_t workspace_bytes, void* stream) {
-  const int W = 2 * Hk * dk + Hv * dv;
-  if (ld_mixed == 0) ld_mixed = W;
-  CLEF_REQUIRE(mixed && conv_w && v_conv, "DeltaNet scan (conv): null mixed, conv weights or v_conv");
-  CLEF_REQUIRE(taps == 4, "DeltaNet scan (conv): 4 taps");
-  CLEF_REQUIRE(dk == dv && dk % 8 == 0, "DeltaNet scan (conv): dk == dv, a multiple of 8");
-  CLEF_REQUIRE(ld_mixed >= W && ld_mixed % 8 == 0, "DeltaNet scan (conv): ld_mixed >= 2 Hk dk + Hv dv, a multiple of 8");
-  CLEF_REQUIRE(((reinterpret_cast<uintptr_t>(mixed) | reinterpret_cast<uintptr_t>(conv_w) |
-                 reinterpret_cast<uintptr_t>(v_conv)) & 15) == 0,
-               "DeltaNet scan (conv): mixed, conv weights and v_conv 16-byte aligned");
-  CLEF_REQUIRE(history_rows >= 0 && history_rows <= taps - 1 && history_stride >= 0,
-               "DeltaNet scan (conv): history rows in 0..3, stride >= 0");
-  CLEF_REQUIRE(initial_stride >= 0, "DeltaNet scan (conv): negative initial-state stride");
-  {  // the prepare reads mixed while it writes v_conv
-    const size_t e = dtype_qkv == CLEF_F32 ? 4 : 2;
-    const uintptr_t m0 = reinterpret_cast<uintptr_t>(mixed), m1 = m0 + e * static_cast<size_t>(T) * ld_mixed;
-    const uintptr_t v0 = reinterpret_cast<uintptr_t>(v_conv), v1 = v0 + e * static_cast<size_t>(T) * Hv * dv;
-    CLEF_REQUIRE(v1 <= m0 || m1 <= v0, "DeltaNet scan (conv): v_conv overlaps mixed");
-  }
-  const bool ragged = cu_seqlens != nullptr;
-  if (ragged) {
-    CLEF_REQUIRE(nseq >= 1 && nseq <= 4096, "DeltaNet scan (conv): 1 <= nseq <= 4096");
-    CLEF_REQUIRE(capture == 0, "DeltaNet scan (conv): no capture in a ragged batch");
-  } else {
-    CLEF_REQUIRE(capture >= 0 && capture <= T, "DeltaNet scan (conv): capture must be in 0..T");
-    CLEF_REQUIRE(capture == 0 || captured, "DeltaNet scan (conv): capture requested without a buffer");
-  }
-  const size_t e = dtype_qkv == CLEF_F32 ? 4 : 2;
-  const char* m = static_cast<const char*>(mixed);
-  clef::ScanParams p;
-  if (int rc = scan_params(p, m, m + e * Hk * dk, v_conv, ld_mixed, static_cast<int64_t>(Hv) * dv, dtype_qkv, g, beta,
-                           sgb, dtype_gb, T, Hk, Hv, dk, dv, chunk, precision, out, so, dtype_out, workspace,
-                           workspace_bytes, ragged ? nseq : 0))
-    return rc;
-  p.initial = initial;
-  if (ragged) {
-    p.init_stride = initial_stride;
-    p.cu_seqlens = cu_seqlens;
-  } else {
-    p.capture = capture;
-    p.captured = captured;
-  }
-  p.final_state = final_states;
-  p.mixed = mixed;
-  p.ld_mixed = ld_mixed;
-  p.conv_w = conv_w;
-  p.conv_hist = history_rows > 0 ? history : nullptr;
-  p.hist_rows = history_rows;
-  p.hist_stride = history_stride;
-  p.conv_channels = W;
-  clef::scan_carve_workspace(p, workspace, precision);
-  return clef::scan_launch(p, precision, static_cast<hipStream_t>(stream));
-}
-
 // The ragged launch tables on the host, by the device kernels' own steps
 // (ragged.hpp) run for every thread index in turn.
 extern "C" int clef_ragged_plan(const int32_t* cu_seqlens, int nseq, int T, int unit, int32_t* spans,

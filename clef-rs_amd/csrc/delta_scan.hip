@@ -13,11 +13,11 @@ namespace {
 int dk_pad(int dk) { return dk <= 32 ? 32 : dk <= 64 ? 64 : 128; }
 
 // Workspace (every region 256-byte aligned; a block is 1 KiB):
-//   Kf, Qf [chunks][Hk] x 64*DK*ct bytes; Uf [chunks][Hv] x DK*64*ct;
-//   Nf [chunks][Hv] x 64*64*ct; sc [chunks][Hv] x 1 KiB; Ucf [Hv] x DK*64*ct;
+//   Uf [chunks][Hv] x DK*64*ct bytes; Nf [chunks][Hv] x 64*64*ct;
+//   sc [chunks][Hv] x 1 KiB; Ucf [Hv] x DK*64*ct;
 //   ragged batches (nseq > 0): chunk_tab, seq_tab, the chunk count.  A batch
 //   of nseq sequences and T tokens has at most T/64 + nseq chunks.
-size_t carve(ScanParams* p, char* b, int T, int Hk, int Hv, int dk, int precision, int nseq) {
+size_t carve(ScanParams* p, char* b, int T, int Hv, int dk, int precision, int nseq) {
   const size_t nchunks = (size_t)(T + kC - 1) / kC + (nseq > 0 ? nseq : 0);
   const size_t ct = precision == 0 ? 4 : 2;
   const size_t DK = dk_pad(dk);
@@ -28,8 +28,6 @@ size_t carve(ScanParams* p, char* b, int T, int Hk, int Hv, int dk, int precisio
     off += al(bytes);
     return q;
   };
-  char* Kf = take(nchunks * Hk * kC * DK * ct);
-  char* Qf = take(nchunks * Hk * kC * DK * ct);
   char* Uf = take(nchunks * Hv * DK * kC * ct);
   char* Nf = take(nchunks * Hv * kC * kC * ct);
   char* sc = take(nchunks * Hv * 1024);
@@ -43,8 +41,6 @@ size_t carve(ScanParams* p, char* b, int T, int Hk, int Hv, int dk, int precisio
     p->chunk_tab = reinterpret_cast<int2*>(ctab);
     p->seq_tab = reinterpret_cast<int4*>(stab);
     p->nchunk_total = reinterpret_cast<int*>(ntot);
-    p->Kf = Kf;
-    p->Qf = Qf;
     p->Uf = Uf;
     p->Nf = Nf;
     p->sc = reinterpret_cast<float*>(sc);
@@ -82,11 +78,11 @@ __global__ __launch_bounds__(kTabThreads) void scan_tables(const int* __restrict
 }
 
 size_t scan_workspace_bytes(int T, int Hk, int Hv, int dk, int precision, int nseq) {
-  return carve(nullptr, nullptr, T, Hk, Hv, dk, precision, nseq);
+  return carve(nullptr, nullptr, T, Hv, dk, precision, nseq);
 }
 
 void scan_carve_workspace(ScanParams& p, void* ws, int precision) {
-  carve(&p, static_cast<char*>(ws), p.T, p.Hk, p.Hv, p.dk, precision, p.cu_seqlens ? p.nseq : 0);
+  carve(&p, static_cast<char*>(ws), p.T, p.Hv, p.dk, precision, p.cu_seqlens ? p.nseq : 0);
 }
 
 int scan_launch(const ScanParams& p0, int precision, hipStream_t stream) {

@@ -19,22 +19,15 @@
 // zeros instead of dividing by an underflowed prefix product.
 //
 // scan_prepare (grid chunks x Hk, fully parallel) does everything that does
-// not depend on the state and writes it as MFMA operand blocks (64 lanes x
-// 16 bytes, in the order the consumer's lanes read them): K^ and Q^ of the
-// k-head, then per v-head the scalars, U and N.  (I + A)^-1 is formed in f32:
-// 16x16 diagonal blocks by forward substitution, the rest by block forward
-// substitution on MFMA.
+// not depend on the state and writes U and N as MFMA operand blocks (64
+// lanes x 16 bytes, in the order the consumer's lanes read them) plus the
+// per-row scalars.  (I + A)^-1 is formed in f32: 16x16 diagonal blocks by
+// forward substitution, the rest by block forward substitution on MFMA.
 //
 // scan_carry (grid Hv x ceil(dv/16)) runs the chunks in order for one v-head
-// and 16 value columns (the columns of S evolve independently):
-//   wave 0  the recurrence X = K^ S, Y, S' = el S + U Y.  S stays in MFMA
-//           accumulators and re-enters the next product as an operand
-//           without leaving the registers (see slot_index);
-//   wave 1  loads K^, U and the scalars of chunk i+2 into a 3-slot LDS ring
-//           with global->LDS DMA (2 slots for f32 operands);
-//   waves 2-3  O of chunk i-1 from the S and Y wave 0 hands over in LDS.
-// One barrier per chunk.  Work-groups sharing a k-head are placed on one XCD
-// so its rows come from that XCD's L2.
+// and 16 value columns (the columns of S evolve independently), reading the
+// raw key and query rows: K^ S and Q^ S are the raw products times per-row
+// factors (see the carry below).
 #pragma once
 #include "common.hpp"
 #include "scan.hpp"
@@ -215,93 +208,13 @@ __device__ __forceinline__ void chunk_at(const ScanParams& p, int c, int& t0, in
   }
 }
 
-// ---------------------------------------------------------------------------
-// Conv prologue (ScanParams::mixed): the mixer's causal conv + SiLU computed
-// where its outputs are consumed, in the separate conv kernel's order and
-// roundings (taps oldest -> newest, each product and sum rounded, hardware
-// SiLU, the result rounded to the input dtype), so the scan sees the same q,
-// k and v values.
-
-// Sequence of token t and its first token (one sequence: 0 and 0).
-__device__ __forceinline__ void conv_sequence(const ScanParams& p, int t, int& seq, int& start) {
-  seq = 0;
-  start = 0;
-  if (!p.cu_seqlens) return;
-  int lo = 0, hi = p.nseq - 1;  // the last s with cu_seqlens[s] <= t
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.cu_seqlens[mid] <= t)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  seq = lo;
-  start = p.cu_seqlens[lo];
-}
-
-// Channels ch .. ch+VI-1 of token tp: a row of `mixed` (clamped to `last`,
-// the chunk's last token) from the sequence start on, before it the
-// sequence's history rows, before those zero (a zero product added to the
-// running sum leaves it unchanged, as skipping the tap does).
-template <class IT>
-__device__ __forceinline__ void conv_load(const ScanParams& p, int tp, int last, int seq, int start, int ch,
-                                          float* x) {
-  constexpr int VI = Vec16<IT>::n;
-  if (tp >= start) {
-    const IT* row = static_cast<const IT*>(p.mixed) + (int64_t)min(tp, last) * p.ld_mixed + ch;
-    const typename Vec16<IT>::type v = *reinterpret_cast<const typename Vec16<IT>::type*>(row);
-#pragma unroll
-    for (int i = 0; i < VI; ++i) x[i] = static_cast<float>(v[i]);
-    return;
-  }
-  const int hr = p.hist_rows + (tp - start);
-  if (p.conv_hist && hr >= 0) {
-    const float* h = p.conv_hist + (int64_t)seq * p.hist_stride + (int64_t)hr * p.conv_channels + ch;
-#pragma unroll
-    for (int i = 0; i < VI; ++i) x[i] = h[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < VI; ++i) x[i] = 0.0f;
-  }
-}
-
-// RPT consecutive rows (chunk rows r0 .. r0+RPT-1) of VI channels from ch:
-// y[j][i] = round_IT(silu(sum_tap x[t-3+tap] w[tap])); rows past the chunk's
-// n tokens and inactive lanes give 0.
-template <class IT, int RPT>
-__device__ __forceinline__ void conv_rows(const ScanParams& p, int t0, int n, int r0, int seq, int start, int ch,
-                                          bool active, float (*y)[Vec16<IT>::n]) {
-  constexpr int VI = Vec16<IT>::n;
-  float w[VI][4];
-  float xr[RPT + 3][VI];
-  if (active) {
-#pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      const float4_t w4 = *reinterpret_cast<const float4_t*>(p.conv_w + (int64_t)(ch + i) * 4);
-#pragma unroll
-      for (int tap = 0; tap < 4; ++tap) w[i][tap] = w4[tap];
-    }
-#pragma unroll
-    for (int k = 0; k < RPT + 3; ++k) conv_load<IT>(p, t0 + r0 + k - 3, t0 + n - 1, seq, start, ch, xr[k]);
-  }
-#pragma unroll
-  for (int j = 0; j < RPT; ++j) {
-#pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int tap = 0; tap < 4; ++tap) acc = add_rn(acc, mul_rn(xr[j + tap][i], w[i][tap]));
-      const float v = silu_hw(acc);
-      y[j][i] = (active && r0 + j < n) ? (sizeof(IT) == 2 ? static_cast<float>(to_f16(v)) : v) : 0.0f;
-    }
-  }
-}
 
 // l2 normalisation of one row held by TPR consecutive lanes (VI values each),
 // eps inside the sqrt (qwen.rs:837-840), times the query scale for q; the
-// explicit fmaf steps fix the association for every caller.
+// explicit fmaf steps fix the association for every caller.  Returns the
+// factor the row was multiplied by.
 template <class CT, int VI, int TPR>
-__device__ __forceinline__ void l2norm_row(const float* x, float extra, CT* dst) {
+__device__ __forceinline__ float l2norm_row(const float* x, float extra, CT* dst) {
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < VI; ++i) s = fmaf(x[i], x[i], s);
@@ -317,12 +230,16 @@ __device__ __forceinline__ void l2norm_row(const float* x, float extra, CT* dst)
     else
       dst[i] = v;
   }
+  return scale;
 }
 
-// Kernel 1: per (chunk, k-head) preparation of every state-independent
-// operand of the chunk, for all v-heads of the k-head.
 // ---------------------------------------------------------------------------
-template <class CT, class IT, int DK, bool CONV>
+// Kernel 1: per (chunk, k-head) preparation of the state-independent operands
+// of the chunk, for all v-heads of the k-head: U and N blocks and the per-row
+// scalars (the normalised keys and queries themselves are not stored: the
+// carry multiplies the raw rows and applies the norms as row factors).
+// ---------------------------------------------------------------------------
+template <class CT, class IT, int DK>
 __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   typedef Geo<CT, DK> G;
   constexpr int EPF = G::EPF, KB = G::KB, TPK = G::TPK, NKX = G::NKX, NKT = G::NKT, NST = G::NST;
@@ -346,6 +263,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   __shared__ __attribute__((aligned(16))) float sBeta[kC];
   __shared__ __attribute__((aligned(16))) float sW[kC];   // exp(gam_last - gam)
   __shared__ __attribute__((aligned(16))) float sWc[kC];  // capture weights
+  __shared__ __attribute__((aligned(16))) float sInv[2][kC];  // row factors: keys 1/|k|, queries qscale/|q|
   CT* sK = reinterpret_cast<CT*>(sR);
   CT* sQ = sK + kC * LDR;
   float* sA = reinterpret_cast<float*>(sR);   // A, row-major [r][c]
@@ -359,7 +277,6 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   int t0, n;
   if (!chunk_span(p, chunk, t0, n)) return;  // grid sized for the most chunks a batch can have
   const int dk = p.dk;
-  const int64_t ck = (int64_t)chunk * p.Hk + hk;
   const int cap_chunk = p.capture > 0 ? (p.capture - 1) / kC : -1;
   const int cap_row = p.capture > 0 ? (p.capture - 1) % kC : 0;
 
@@ -370,24 +287,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     gbits = load_bits(p.g, gi, p.dtype_gb);
     bbits = load_bits(p.beta, gi, p.dtype_gb);
   }
-  if constexpr (CONV) {
-    // the conv prologue: lane group g (TPR lanes) holds chunk rows
-    // RPT g .. RPT g + RPT - 1 of k, then of q, VI channels per lane
-    constexpr int RPT = TPR / 4;
-    const int g = tid / TPR, e0 = (tid % TPR) * VI;
-    int seq, start;
-    conv_sequence(p, t0, seq, start);
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const bool isq = m == 1;
-      const int ch = (isq ? 0 : p.Hk * dk) + hk * dk + e0;  // [q | k | v] channels
-      float y[RPT][VI];
-      conv_rows<IT, RPT>(p, t0, n, RPT * g, seq, start, ch, e0 < dk, y);
-#pragma unroll
-      for (int j = 0; j < RPT; ++j)
-        l2norm_row<CT, VI, TPR>(y[j], isq ? p.qscale : 1.0f, (isq ? sQ : sK) + (RPT * g + j) * LDR + e0);
-    }
-  } else {
+  {
     const IT* qbase = static_cast<const IT*>(p.q);
     const IT* kbase = static_cast<const IT*>(p.k);
     typename Vec16<IT>::type raw[NPASS];
@@ -409,31 +309,19 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       float x[VI];
 #pragma unroll
       for (int i = 0; i < VI; ++i) x[i] = (r < n && e0 + i < dk) ? static_cast<float>(raw[ps][i]) : 0.0f;
-      l2norm_row<CT, VI, TPR>(x, isq ? p.qscale : 1.0f, (isq ? sQ : sK) + r * LDR + e0);
+      const float f = l2norm_row<CT, VI, TPR>(x, isq ? p.qscale : 1.0f, (isq ? sQ : sK) + r * LDR + e0);
+      if (tid % TPR == 0) sInv[isq][r] = r < n ? f : 0.0f;
     }
   }
   lds_barrier();
 
-  // ---- 2. K^ / Q^ operand blocks, K^ transposed, Gram tiles
-  {
-    frag* kf = static_cast<frag*>(p.Kf) + ck * G::NBK * 64 + lane;
-    frag* qf = static_cast<frag*>(p.Qf) + ck * G::NBK * 64 + lane;
-    for (int blk = wave; blk < 2 * G::NBK; blk += 4) {
-      const bool isq = blk >= G::NBK;
-      const int b = isq ? blk - G::NBK : blk;
-      const int t = b / NKX, kb = b % NKX;
-      // K^ rows in slot order (rows of X = K^ S), Q^ rows in token order
-      const int row = isq ? 16 * t + col : slot_index<CT>(t, col);
-      const frag f = load_frag<CT>((isq ? sQ : sK) + row * LDR + kb * KB + grp * EPF);
-      (isq ? qf : kf)[b * 64] = f;
-    }
-    for (int it = tid; it < DK * (kC / EPF); it += 256) {
-      const int e = it / (kC / EPF), tok0 = (it % (kC / EPF)) * EPF;
-      frag f;
+  // ---- 2. K^ transposed, Gram tiles
+  for (int it = tid; it < DK * (kC / EPF); it += 256) {
+    const int e = it / (kC / EPF), tok0 = (it % (kC / EPF)) * EPF;
+    frag f;
 #pragma unroll
-      for (int j = 0; j < EPF; ++j) f[j] = sK[(tok0 + j) * LDR + e];
-      *reinterpret_cast<frag*>(sKT + e * LDT + tok0) = f;
-    }
+    for (int j = 0; j < EPF; ++j) f[j] = sK[(tok0 + j) * LDR + e];
+    *reinterpret_cast<frag*>(sKT + e * LDT + tok0) = f;
   }
   // 20 lower 16x16 tiles: K^K^T (jobs 0-9) and Q^K^T (jobs 10-19), 5 per wave
   float4_t gram[5];
@@ -466,7 +354,9 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   for (int v = 0; v < rep; ++v) {
     const int h = hk * rep + v;
     const int64_t cv = (int64_t)chunk * p.Hv + h;
-    // 3a. cumulative decay and the per-row factors (wave 0, lane = token)
+    // 3a. cumulative decay and the per-row factors (wave 0, lane = token):
+    //     the carry's row factors 1/|k| e^gam (for V - e^gam K^ S) and
+    //     qscale/|q| e^gam (for e^gam Q^ S), gam (capture) and e^gam
     if (wave == 0) {
       const float gv = lane < n ? bits_to_f32(gbits, p.dtype_gb) : 0.0f;
       const float bv = lane < n ? bits_to_f32(bbits, p.dtype_gb) : 0.0f;
@@ -487,11 +377,12 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       sBeta[lane] = bv;
       sW[lane] = decay_exp(gl - cs);
       if (chunk == cap_chunk) sWc[lane] = lane <= cap_row ? decay_exp(gcap - cs) : 0.0f;
+      const float eg = decay_exp(cs);
       float* sc = p.sc + cv * 256;
-      sc[lane] = bv;
-      sc[64 + lane] = decay_exp(cs);
+      sc[lane] = sInv[0][lane] * eg;
+      sc[64 + lane] = sInv[1][lane] * eg;
       sc[128 + lane] = cs;
-      sc[192 + lane] = 0.0f;
+      sc[192 + lane] = eg;
     }
     lds_barrier();
     // 3b. A (f32) and M (CT) from the Gram tiles
@@ -618,49 +509,75 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     lds_barrier();  // before the next v-head rewrites sA, sTT, sM, sGam
   }
 
-  if constexpr (CONV) {
-    // ---- 4. the convolved v of this k-head's v-heads, for the carry
-    // (rows of this chunk only; p.v has token stride p.sv, dv == dk)
-    constexpr int RPT = TPR / 4;
-    const int g = tid / TPR, e0 = (tid % TPR) * VI;
-    int seq, start;
-    conv_sequence(p, t0, seq, start);
-    IT* vout = static_cast<IT*>(const_cast<void*>(p.v));
-    for (int v = 0; v < rep; ++v) {
-      const int h = hk * rep + v;
-      const int ch = 2 * p.Hk * dk + h * p.dv + e0;
-      float y[RPT][VI];
-      conv_rows<IT, RPT>(p, t0, n, RPT * g, seq, start, ch, e0 < p.dv, y);
-#pragma unroll
-      for (int j = 0; j < RPT; ++j) {
-        const int r = RPT * g + j;
-        if (r < n && e0 < p.dv) {
-          typename Vec16<IT>::type o;
-#pragma unroll
-          for (int i = 0; i < VI; ++i) o[i] = static_cast<IT>(y[j][i]);  // exact: y holds IT values
-          *reinterpret_cast<typename Vec16<IT>::type*>(vout + (int64_t)(t0 + r) * p.sv + (int64_t)h * p.dv + e0) = o;
-        }
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
 // Kernel 2: sequential chunk carry for one (v-head, 16 value columns).
+//
+// Wave 0 runs the recurrence; loader waves fill a ring of LDS slots, D0 - 1
+// chunks ahead, with global->LDS DMA (f16: wave 1 the chunk's raw key rows,
+// wave 2 its U blocks and row scalars; f32: wave 1 both); output waves form
+// the outputs of the previous chunk (f16: four waves of one 16-row tile, f32:
+// two of two) from the S and Y that wave 0 hands over in LDS and from query
+// rows and N blocks they load into registers a few chunks ahead.  One
+// barrier per chunk.
+//
+// Norms as row factors: with a_r = 1/|k_r| and b_r = qscale/|q_r|,
+//   e^gam (K^ S) = diag(a e^gam) (K S),   e^gam (Q^ S) = diag(b e^gam) (Q S),
+// so the raw key and query rows (the conv output, as stored) are the MFMA
+// operands and nothing normalised is written to memory.
 // ---------------------------------------------------------------------------
-template <class CT, int DK>
+
+// XOR swizzle of the 16-byte chunk index of a raw key row in LDS, so that the
+// 16 rows one MFMA fragment read touches (slot-ordered rows for f16, which
+// differ in row bits 0, 1, 3, 4; consecutive rows for f32) hit distinct banks
+// for every row width (NCH chunks of 16 bytes per row).
+template <class CT, int NCH>
+__device__ __forceinline__ int kswz(int r) {
+  if constexpr (sizeof(CT) == 2) {
+    if constexpr (NCH >= 16) return (r & 3) | ((r >> 1) & 12);
+    else if constexpr (NCH == 8) return ((r >> 1) & 1) | ((r >> 2) & 6);
+    else return (r >> 3) & 3;
+  } else {
+    if constexpr (NCH >= 16) return r & 15;
+    else if constexpr (NCH == 8) return (r >> 1) & 7;
+    else return (r >> 2) & 3;
+  }
+}
+
+template <class CT, class IT, int DK>
 struct Carry {
   typedef Geo<CT, DK> G;
   typedef typename Mma<CT>::frag frag;
-  static constexpr int D0 = sizeof(CT) == 2 ? 3 : 2;   // ring slots
-  static constexpr int NL = G::NBK + G::NBU + 1;       // blocks per slot (+ scalars)
-  static constexpr int NH = G::NKX + G::NKT;           // hand-off blocks: S, Y
-  static constexpr int SLOT = NL * 64;                 // ring slot, 16-byte units
-  static_assert((D0 - 2) * NL < 64, "ring wait count must fit vmcnt");
+  static constexpr int RB = DK * (int)sizeof(IT);        // bytes of a raw key row
+  static constexpr int NCH = RB / 16;                     // its 16-byte chunks
+  static constexpr int KBYTES = kC * RB;                  // a chunk's raw keys
+  static constexpr int NDK = KBYTES / 1024;               // 1 KiB DMA instructions for them
+  static constexpr int UOFF = KBYTES;                     // U blocks within a slot
+  static constexpr int SOFF = KBYTES + G::NBU * 1024;     // row scalars within a slot
+  static constexpr int SLOT = SOFF + 1024;
+  static constexpr int HAND = 2 * (G::NKX + G::NKT) * 1024;  // S and Y hand-off, double buffered
+  static constexpr int LDS = 160 * 1024;
+  static constexpr int OD = 2;                            // chunks of output operands in registers
+  // waves: the recurrence, NLOAD loaders, NOUT output waves of TPW 16-row tiles
+  // (f32 operands take four waves in all, so each may hold 512 registers)
+  static constexpr int NLOAD = sizeof(CT) == 2 ? 2 : 1;
+  // ring slots: at most 4, as many as the LDS holds, and few enough that the
+  // DMA instructions a loader keeps in flight fit the 6-bit vmcnt
+  static constexpr int PERW = NLOAD == 1 ? NDK + G::NBU + 1 : (NDK > G::NBU + 1 ? NDK : G::NBU + 1);
+  static constexpr int DL = (LDS - HAND) / SLOT, DV = 2 + 63 / PERW;
+  static constexpr int D0 = DL < DV ? (DL < 4 ? DL : 4) : (DV < 4 ? DV : 4);
+  static constexpr int NOUT = sizeof(CT) == 2 ? 4 : 2;
+  static constexpr int TPW = 4 / NOUT;
+  static constexpr int THREADS = 64 * (1 + NLOAD + NOUT);
+  static_assert(D0 >= 2 && D0 * SLOT + HAND <= LDS, "two ring slots fit the LDS");
+  static_assert(NLOAD == 2 ? (D0 - 2) * NDK < 64 && (D0 - 2) * (G::NBU + 1) < 64
+                           : (D0 - 2) * (NDK + G::NBU + 1) < 64, "ring wait counts fit vmcnt");
+  static_assert(KBYTES % 1024 == 0, "whole DMA instructions per chunk of keys");
 };
 
 struct CarryCtx {
-  int h, hk, j0, jc, jcc;
+  int h, hk, j0, jc;
   bool col_ok;
   int lane, col, grp;
   int nchunks, cap_chunk, cap_row;
@@ -669,50 +586,164 @@ struct CarryCtx {
   float* fin;         // its final state or null
 };
 
-// wave 1: K^, U and scalars of chunk i+D0-1 into the ring during chunk i.
-template <class CT, int DK, bool VL>
-__device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x,
-                                             typename Carry<CT, DK>::frag* ring) {
-  typedef Carry<CT, DK> K;
-  typedef typename K::G G;
+// EPF elements k.. of raw key row r in a slot's key region, as a CT fragment.
+template <class CT, class IT, int DK>
+__device__ __forceinline__ typename Mma<CT>::frag key_frag(const char* keys, int r, int k) {
+  constexpr int RB = DK * (int)sizeof(IT), NCH = RB / 16;
+  const char* row = keys + r * RB;
+  const int key = kswz<CT, NCH>(r);
+  if constexpr (sizeof(CT) == sizeof(IT)) {
+    const int c = (k * (int)sizeof(IT)) >> 4;
+    return *reinterpret_cast<const typename Mma<CT>::frag*>(row + ((c ^ key) << 4));
+  } else if constexpr (sizeof(IT) == 2) {  // f16 keys, f32 fragment of 4
+    const int b = k * 2, c = b >> 4;
+    const half4 v = *reinterpret_cast<const half4*>(row + ((c ^ key) << 4) + (b & 15));
+    return float4_t{static_cast<float>(v[0]), static_cast<float>(v[1]), static_cast<float>(v[2]),
+                    static_cast<float>(v[3])};
+  } else {  // f32 keys, f16 fragment of 8 (two chunks)
+    const int c = (k * 4) >> 4;
+    const float4_t a = *reinterpret_cast<const float4_t*>(row + ((c ^ key) << 4));
+    const float4_t b = *reinterpret_cast<const float4_t*>(row + (((c + 1) ^ key) << 4));
+    half8 f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[i] = static_cast<half_t>(a[i]);
+      f[4 + i] = static_cast<half_t>(b[i]);
+    }
+    return f;
+  }
+}
+
+// EPF elements k.. of a raw query row in global memory as a CT fragment;
+// elements past dk read as zero (VEC: dk == DK and 16-byte rows).  VEC is a
+// template parameter: a run-time choice inside the prefetching loop makes the
+// compiler wait for every load where the two paths join.
+template <class CT, class IT, bool VEC>
+__device__ __forceinline__ typename Mma<CT>::frag query_frag(const IT* row, int k, int dk) {
+  constexpr int EPF = 16 / (int)sizeof(CT);
+  typename Mma<CT>::frag f;
+  if constexpr (VEC) {
+    if constexpr (sizeof(CT) == sizeof(IT)) {
+      return *reinterpret_cast<const typename Mma<CT>::frag*>(row + k);
+    } else if constexpr (sizeof(IT) == 2) {
+      const half4 v = *reinterpret_cast<const half4*>(row + k);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[i] = static_cast<float>(v[i]);
+      return f;
+    } else {
+      const float4_t a = *reinterpret_cast<const float4_t*>(row + k);
+      const float4_t b = *reinterpret_cast<const float4_t*>(row + k + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[i] = static_cast<half_t>(a[i]);
+        f[4 + i] = static_cast<half_t>(b[i]);
+      }
+      return f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPF; ++i) f[i] = static_cast<CT>(k + i < dk ? static_cast<float>(row[k + i]) : 0.0f);
+    return f;
+  }
+}
+
+// Wave 1: the raw key rows of chunk c into `keys`.  DMA instruction q, lane l
+// writes slot bytes 1024 q + 16 l, i.e. row r = (1024 q + 16 l) / RB at
+// swizzled chunk pc; it reads logical chunk pc ^ kswz(r) of that row (rows
+// past the chunk's end repeat its last row, whose results are multiplied by
+// a zero row factor).  Without whole 16-byte rows (dk < DK or unaligned
+// rows) the rows are loaded element by element and stored with zeros past dk.
+template <class CT, class IT, int DK, bool VL>
+__device__ __forceinline__ void carry_keys(const ScanParams& p, const CarryCtx& x, char* keys, int c,
+                                           bool fast) {
+  typedef Carry<CT, IT, DK> K;
+  int t0, n;
+  chunk_at<VL>(p, (VL ? x.c0 : 0) + c, t0, n);
+  const char* base = reinterpret_cast<const char*>(static_cast<const IT*>(p.k) + (int64_t)t0 * p.sqk +
+                                                   (int64_t)x.hk * p.dk);
+  const int64_t rowb = p.sqk * (int64_t)sizeof(IT);
+  if (fast) {
+#pragma unroll
+    for (int q = 0; q < K::NDK; ++q) {
+      const int o = 1024 * q + 16 * x.lane, r = o / K::RB, pc = (o % K::RB) >> 4;
+      const int lc = pc ^ kswz<CT, K::NCH>(r);
+      dma_block(base + min(r, n - 1) * rowb + (lc << 4), keys + 1024 * q);
+    }
+  } else {
+    constexpr int VI = 16 / (int)sizeof(IT);
+    for (int q = 0; q < K::NDK; ++q) {
+      const int o = 1024 * q + 16 * x.lane, r = o / K::RB, pc = (o % K::RB) >> 4;
+      const int e0 = (pc ^ kswz<CT, K::NCH>(r)) * VI;
+      const IT* row = reinterpret_cast<const IT*>(base + min(r, n - 1) * rowb);
+      typename Vec16<IT>::type v;
+#pragma unroll
+      for (int i = 0; i < VI; ++i) v[i] = e0 + i < p.dk ? row[e0 + i] : IT(0);
+      *reinterpret_cast<typename Vec16<IT>::type*>(keys + o) = v;
+    }
+  }
+}
+
+// Wave 2: the U blocks and row scalars of chunk c into the slot.
+template <class CT, class IT, int DK, bool VL>
+__device__ __forceinline__ void carry_ublocks(const ScanParams& p, const CarryCtx& x, char* slot, int c) {
+  typedef Carry<CT, IT, DK> K;
+  const int64_t cg = (VL ? x.c0 : 0) + c;
+  const char* uf = static_cast<const char*>(p.Uf) + ((cg * p.Hv + x.h) * K::G::NBU * 64 + x.lane) * 16;
+  const char* sc = reinterpret_cast<const char*>(p.sc + (cg * p.Hv + x.h) * 256) + x.lane * 16;
+#pragma unroll
+  for (int b = 0; b < K::G::NBU; ++b) dma_block(uf + b * 1024, slot + K::UOFF + b * 1024);
+  dma_block(sc, slot + K::SOFF);
+}
+
+template <class CT, class IT, int DK, bool VL>
+__device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x, int wave, char* ring) {
+  typedef Carry<CT, IT, DK> K;
+  const bool fast = p.vec_qk && p.dk == DK;
+  const bool keys = K::NLOAD == 1 || wave == 1, ublocks = K::NLOAD == 1 || wave == 2;
+  // outstanding DMA instructions per chunk for this wave (fast key path)
+  constexpr int PER = K::NLOAD == 1 ? K::NDK + K::G::NBU + 1 : 0;
+  auto slot = [&](int c) { return ring + (c % K::D0) * K::SLOT; };
   auto issue = [&](int c) {
-    typename K::frag* slot = ring + (c % K::D0) * K::SLOT;
-    const int64_t cg = (VL ? x.c0 : 0) + c;
-    const char* kf = static_cast<const char*>(p.Kf) + ((cg * p.Hk + x.hk) * G::NBK * 64 + x.lane) * 16;
-    const char* uf = static_cast<const char*>(p.Uf) + ((cg * p.Hv + x.h) * G::NBU * 64 + x.lane) * 16;
-    const char* sc = reinterpret_cast<const char*>(p.sc + (cg * p.Hv + x.h) * 256) + x.lane * 16;
-#pragma unroll
-    for (int b = 0; b < G::NBK; ++b) dma_block(kf + b * 1024, slot + b * 64);
-#pragma unroll
-    for (int b = 0; b < G::NBU; ++b) dma_block(uf + b * 1024, slot + (G::NBK + b) * 64);
-    dma_block(sc, slot + (G::NBK + G::NBU) * 64);
+    if (keys && fast) carry_keys<CT, IT, DK, VL>(p, x, slot(c), c, true);
+    if (ublocks) carry_ublocks<CT, IT, DK, VL>(p, x, slot(c), c);
   };
   for (int c = 0; c < K::D0 - 1; ++c)
     if (c < x.nchunks) issue(c);
+  if (keys && !fast) carry_keys<CT, IT, DK, VL>(p, x, slot(0), 0, false);
   wait_vmcnt<0>();
   lds_barrier();  // prologue
   for (int i = 0; i < x.nchunks; ++i) {
     if (i + K::D0 - 1 < x.nchunks) {
       issue(i + K::D0 - 1);
-      wait_vmcnt<(K::D0 - 2) * K::NL>();  // chunk i+1 has landed
+      // chunk i+1 has landed
+      if constexpr (K::NLOAD == 1)
+        wait_vmcnt<(K::D0 - 2) * PER>();
+      else if (wave == 1)
+        wait_vmcnt<(K::D0 - 2) * K::NDK>();
+      else
+        wait_vmcnt<(K::D0 - 2) * (K::G::NBU + 1)>();
     } else {
       wait_vmcnt<0>();
     }
+    if (keys && !fast && i + 1 < x.nchunks) carry_keys<CT, IT, DK, VL>(p, x, slot(i + 1), i + 1, false);
     lds_barrier();  // end of chunk i
   }
   lds_barrier();  // outputs of the last chunk
 }
 
-// wave 0: the recurrence.  IT = dtype of v.
-template <class CT, int DK, class IT, bool VL>
-__device__ __forceinline__ void carry_recurrence(const ScanParams& p, const CarryCtx& x,
-                                                 const typename Carry<CT, DK>::frag* ring,
-                                                 typename Carry<CT, DK>::frag* hand) {
-  typedef Carry<CT, DK> K;
+// Wave 0: the recurrence.  Per chunk i (slot i % D0):
+//   X = K S (raw keys, rows in slot order), Y = V - (a e^gam) X,
+//   S <- e^gam_last S + U Y;
+// S_i and Y_i go to the output waves through `hand`.
+template <class CT, class IT, int DK, bool VL, bool CAP>
+__device__ __forceinline__ void carry_recurrence(const ScanParams& p, const CarryCtx& x, const char* ring,
+                                                 typename Mma<CT>::frag* hand) {
+  typedef Carry<CT, IT, DK> K;
   typedef typename K::G G;
   typedef typename K::frag frag;
-  constexpr int NST = G::NST, NKX = G::NKX, NKT = G::NKT, NBK = G::NBK, NBU = G::NBU, TPK = G::TPK;
-  const int lane = x.lane, grp = x.grp;
+  constexpr int NST = G::NST, NKX = G::NKX, NKT = G::NKT, NBU = G::NBU, TPK = G::TPK, KB = G::KB;
+  constexpr int EPF = G::EPF;
+  const int lane = x.lane, grp = x.grp, col = x.col;
   const int dk = p.dk, dv = p.dv;
   const float* init = VL ? x.init : p.initial;
   float* fin = VL ? x.fin : p.final_state;
@@ -731,92 +762,86 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
 #pragma unroll
   for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
 
+  // v two chunks ahead in registers (this lane's 16 X-rows); rows past the
+  // end of the sequence fall outside the buffer range (read 0), and so do
+  // columns past dv: their lanes add 2^31 to every offset (a chunk's range
+  // is at most 64 rows of 2^22 four-byte elements, 2^30 bytes, so the sum
+  // stays in 32 bits and past the range).  Branch-free offsets keep the loads
+  // unconditional, so they stay in flight across the loop.
   const IT* vbase = static_cast<const IT*>(p.v) + (int64_t)x.h * dv + x.j0;
-  // byte offsets of this lane's 16 X-rows within a chunk of v; rows past the
-  // end of the sequence fall outside the chunk's buffer range and read 0
-  int voff[16];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      voff[4 * t + i] = x.col_ok ? (slot_index<CT>(t, 4 * grp + i) * (int)p.sv + x.col) * (int)sizeof(IT) : kOOB;
+  const uint32_t vlane = (uint32_t)col * (uint32_t)sizeof(IT) + (x.col_ok ? 0u : 0x80000000u);
+  const uint32_t vrow = (uint32_t)p.sv * (uint32_t)sizeof(IT);
   auto load_v = [&](uint32_t* vb, int c) {
     int t0, n;
     chunk_at<VL>(p, (VL ? x.c0 : 0) + min(c, x.nchunks - 1), t0, n);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(vbase + (int64_t)t0 * p.sv, n * (int)p.sv * (int)sizeof(IT));
 #pragma unroll
-    for (int k = 0; k < 16; ++k) vb[k] = buffer_load_bits<IT>(r, voff[k]);
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        vb[4 * t + j] = buffer_load_bits<IT>(r, (int)((uint32_t)slot_index<CT>(t, 4 * grp + j) * vrow + vlane));
   };
   uint32_t va[16], vb[16];
   load_v(va, 0);
   load_v(vb, 1);
+  // this lane's key rows (slot order) and k offset within each k-block
+  int krow[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) krow[t] = slot_index<CT>(t, col);
   lds_barrier();  // prologue
 
   auto step = [&](int i, uint32_t* vbuf) {
-    const frag* slot = ring + (i % K::D0) * K::SLOT;
-    const float* scs = reinterpret_cast<const float*>(slot + (NBK + NBU) * 64);  // beta, eg, gam
-    // every LDS operand of the chunk is requested before the first product,
-    // so the reads overlap each other and the MFMAs instead of serialising
-    frag kfr[4][NKX], ufr[NST][NKT];
-    float4_t eg[4];
+    const char* slot = ring + (i % K::D0) * K::SLOT;
+    const frag* uslot = reinterpret_cast<const frag*>(slot + K::UOFF);
+    const float* scs = reinterpret_cast<const float*>(slot + K::SOFF);  // a e^gam, b e^gam, gam, e^gam
+    frag* hs = hand + (i & 1) * (NKX + NKT) * 64;
+    frag kf[4][NKX];
+    float4_t ya[4], X[4];
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb)
+    for (int t = 0; t < 4; ++t) kf[t][0] = key_frag<CT, IT, DK>(slot, krow[t], grp * EPF);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) kfr[t][kb] = slot[(t * NKX + kb) * 64 + lane];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) eg[t] = *reinterpret_cast<const float4_t*>(scs + 64 + slot_index<CT>(t, 4 * grp));
-    const float el = scs[64 + kC - 1];
-    // hand S_i to the output waves
-    frag* hs = hand + (i & 1) * K::NH * 64;
+    for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    // S_i goes to the output waves
 #pragma unroll
     for (int kb = 0; kb < NKX; ++kb) hs[kb * 64 + lane] = Sf[kb];
     __builtin_amdgcn_sched_barrier(0);
-    // X = K^ S (token rows in slot order)
-    float4_t X[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-    // (rounds of 4 independent accumulators, fenced so the scheduler cannot
-    // turn them into dependent chains)
+    // X = K S in rounds of 4 independent products; each round also requests
+    // the next round's operands
 #pragma unroll
     for (int kb = 0; kb < NKX; ++kb) {
+      if (kb + 1 < NKX) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kfr[t][kb], Sf[kb]);
+        for (int t = 0; t < 4; ++t) kf[t][kb + 1] = key_frag<CT, IT, DK>(slot, krow[t], (kb + 1) * KB + grp * EPF);
+      }
+      if (kb == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ya[t] = *reinterpret_cast<const float4_t*>(scs + slot_index<CT>(t, 4 * grp));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kf[t][kb], Sf[kb]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // U is requested while the products run (its registers replace K^'s)
+    const float el = scs[192 + kC - 1];
+    frag uf[NST][NKT];
 #pragma unroll
     for (int s = 0; s < NST; ++s)
 #pragma unroll
-      for (int b = 0; b < NKT; ++b) ufr[s][b] = slot[(NBK + s * NKT + b) * 64 + lane];
-    __builtin_amdgcn_sched_barrier(0);
-    // Y = V - exp(gam) X (beta is folded into U and N) for token block b
+      for (int b = 0; b < NKT; ++b) uf[s][b] = uslot[(s * NKT + b) * 64 + lane];
+    // Y = V - (a e^gam) X for token block b (beta is folded into U and N)
     frag Yf[NKT];
     auto y_block = [&](int b) {
 #pragma unroll
       for (int u = 0; u < TPK; ++u) {
         const int t = TPK * b + u;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) X[t][j] = bits_value<IT>(vbuf[4 * t + j]) - eg[t][j] * X[t][j];
+        for (int j = 0; j < 4; ++j) X[t][j] = bits_value<IT>(vbuf[4 * t + j]) - ya[t][j] * X[t][j];
       }
       Yf[b] = pack_frag(X, b, CT(0));
     };
-    if (i != x.cap_chunk) {
-      // S <- exp(gam_last) S + U Y: the scaling runs under the X products, and
-      // each token block's update starts as soon as its Y is packed
 #pragma unroll
-      for (int s = 0; s < NST; ++s) S[s] = S[s] * el;
-#pragma unroll
-      for (int b = 0; b < NKT; ++b) {
-        y_block(b);
-#pragma unroll
-        for (int s = 0; s < NST; ++s) Mma<CT>::mma(S[s], ufr[s][b], Yf[b]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else {
-      // capture chunk: the state after token `capture` is
-      // exp(gam_r*) S_i + Ucap Y_i, formed before S_i is updated
-#pragma unroll
-      for (int b = 0; b < NKT; ++b) y_block(b);
+    for (int b = 0; b < NKT; ++b) y_block(b);
+    if (CAP && i == x.cap_chunk) {
+      // state after token `capture`: exp(gam_r*) S_i + Ucap Y_i
       const float ec = decay_exp(scs[128 + x.cap_row]);
       const frag* uc = static_cast<const frag*>(p.Ucf) + (int64_t)x.h * NBU * 64 + lane;
 #pragma unroll
@@ -830,174 +855,22 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
           if (row < dk && x.col_ok) p.captured[((int64_t)x.h * dk + row) * dv + x.jc] = acc[j];
         }
       }
-#pragma unroll
-      for (int s = 0; s < NST; ++s) {
-        S[s] = S[s] * el;
-#pragma unroll
-        for (int b = 0; b < NKT; ++b) Mma<CT>::mma(S[s], ufr[s][b], Yf[b]);
-      }
     }
-#pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
-    // hand Y_i to the output waves
+    // Y_i goes to the output waves
 #pragma unroll
     for (int b = 0; b < NKT; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
-    load_v(vbuf, i + 2);
-    lds_barrier();  // end of chunk i
-  };
-  int i = 0;
-  for (; i + 1 < x.nchunks; i += 2) {
-    step(i, va);
-    step(i + 1, vb);
-  }
-  if (i < x.nchunks) step(i, va);
-  lds_barrier();  // outputs of the last chunk
-
-  if (fin) {
-#pragma unroll
-    for (int s = 0; s < NST; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = slot_index<CT>(s, 4 * grp + j);
-        if (row < dk && x.col_ok) fin[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
-      }
-  }
-}
-
-// wave 0, f16 operands: the recurrence with the LDS reads of each round
-// interleaved with the MFMAs of the previous one (a wave issues one 1 KiB
-// read per ~14 cycles, an MFMA per 18).  IT = dtype of v.
-template <class CT, int DK, class IT, bool VL>
-__device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const CarryCtx& x,
-                                                     const typename Carry<CT, DK>::frag* ring,
-                                                     typename Carry<CT, DK>::frag* hand) {
-  typedef Carry<CT, DK> K;
-  typedef typename K::G G;
-  typedef typename K::frag frag;
-  constexpr int NST = G::NST, NKX = G::NKX, NBK = G::NBK, NBU = G::NBU;
-  static_assert(G::NKT == 2 && G::TPK == 2, "f16 geometry");
-  const int lane = x.lane, grp = x.grp;
-  const int dk = p.dk, dv = p.dv;
-  const float* init = VL ? x.init : p.initial;
-  float* fin = VL ? x.fin : p.final_state;
-
-  float4_t S[NST];
-#pragma unroll
-  for (int s = 0; s < NST; ++s)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = slot_index<CT>(s, 4 * grp + i);
-      float v = 0.0f;
-      if (init && row < dk && x.col_ok) v = init[((int64_t)x.h * dk + row) * dv + x.jc];
-      S[s][i] = v;
-    }
-  frag Sf[NKX];
-#pragma unroll
-  for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
-
-  // v two chunks ahead in registers: byte offsets of this lane's 16 X-rows;
-  // rows past the end of the sequence fall outside the buffer range (read 0)
-  const IT* vbase = static_cast<const IT*>(p.v) + (int64_t)x.h * dv + x.j0;
-  int voff[16];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      voff[4 * q + j] = x.col_ok ? (slot_index<CT>(q, 4 * grp + j) * (int)p.sv + x.col) * (int)sizeof(IT) : kOOB;
-  auto load_v = [&](uint32_t* vb, int c) {
-    int t0, n;
-    chunk_at<VL>(p, (VL ? x.c0 : 0) + min(c, x.nchunks - 1), t0, n);
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(vbase + (int64_t)t0 * p.sv, n * (int)p.sv * (int)sizeof(IT));
-#pragma unroll
-    for (int k = 0; k < 16; ++k) vb[k] = buffer_load_bits<IT>(r, voff[k]);
-  };
-  uint32_t va[16], vb[16];
-  load_v(va, 0);
-  load_v(vb, 1);
-  lds_barrier();  // prologue
-
-  auto step = [&](int i, uint32_t* vbuf) {
-    const frag* slot = ring + (i % K::D0) * K::SLOT;
-    const float* scs = reinterpret_cast<const float*>(slot + (NBK + NBU) * 64);  // beta, eg, gam
-    frag* hs = hand + (i & 1) * K::NH * 64;
-    frag kf[4][NKX], uf[NST][2];
-    float4_t eg[4], X[4];
-    float el;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) kf[t][0] = slot[(t * NKX) * 64 + lane];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
     __builtin_amdgcn_sched_barrier(0);
-    // X = K^ S in rounds of 4 independent products; each round also requests
-    // the next round's operands
+    // S <- exp(gam_last) S + U Y
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) {
-      if (kb + 1 < NKX) {
+    for (int s = 0; s < NST; ++s) S[s] = S[s] * el;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) kf[t][kb + 1] = slot[(t * NKX + kb + 1) * 64 + lane];
-      }
-      if (kb == 0) {
+    for (int b = 0; b < NKT; ++b) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) eg[t] = *reinterpret_cast<const float4_t*>(scs + 64 + slot_index<CT>(t, 4 * grp));
-        el = scs[64 + kC - 1];
-      }
-      if (kb == NKX - 1) {
-#pragma unroll
-        for (int s = 0; s < NST; ++s) uf[s][0] = slot[(NBK + 2 * s) * 64 + lane];
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kf[t][kb], Sf[kb]);
+      for (int s = 0; s < NST; ++s) Mma<CT>::mma(S[s], uf[s][b], Yf[b]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Y = V - exp(gam) X for token block b (beta is folded into U and N)
-    frag Yf[2];
-    auto y_block = [&](int b) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          X[2 * b + u][j] = bits_value<IT>(vbuf[4 * (2 * b + u) + j]) - eg[2 * b + u][j] * X[2 * b + u][j];
-      Yf[b] = pack_frag(X, b, CT(0));
-    };
-    y_block(0);
-    if (i == x.cap_chunk) {
-      // state after token `capture`: exp(gam_r*) S_i + Ucap Y_i
-      y_block(1);
-      const float ec = decay_exp(scs[128 + x.cap_row]);
-      const frag* uc = static_cast<const frag*>(p.Ucf) + (int64_t)x.h * NBU * 64 + lane;
-#pragma unroll
-      for (int s = 0; s < NST; ++s) {
-        float4_t acc = S[s] * ec;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) Mma<CT>::mma(acc, uc[(2 * s + b) * 64], Yf[b]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = slot_index<CT>(s, 4 * grp + j);
-          if (row < dk && x.col_ok) p.captured[((int64_t)x.h * dk + row) * dv + x.jc] = acc[j];
-        }
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // S <- exp(gam_last) S + U Y, token block 0 (requests U of block 1)
-#pragma unroll
-    for (int s = 0; s < NST; ++s) uf[s][1] = slot[(NBK + 2 * s + 1) * 64 + lane];
-#pragma unroll
-    for (int s = 0; s < NST; ++s) {
-      S[s] = S[s] * el;
-      Mma<CT>::mma(S[s], uf[s][0], Yf[0]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (i != x.cap_chunk) y_block(1);
-    // token block 1; S_i goes to the output waves meanwhile
-#pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) hs[kb * 64 + lane] = Sf[kb];
-#pragma unroll
-    for (int s = 0; s < NST; ++s) Mma<CT>::mma(S[s], uf[s][1], Yf[1]);
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
-#pragma unroll
-    for (int b = 0; b < 2; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
     load_v(vbuf, i + 2);
     lds_barrier();  // end of chunk i
   };
@@ -1020,49 +893,52 @@ __device__ __forceinline__ void carry_recurrence_f16(const ScanParams& p, const 
   }
 }
 
-// waves 2-3: O of chunk c during chunk c+1, rows 16t.. for t = 2(wave-2)+{0,1}.
-template <class CT, int DK, class OT, bool VL>
+// Output waves: O of chunk c during chunk c+1, TPW tiles of 16 rows (token
+// order) from row 16 TPW ow: O = diag(b e^gam) (Q S) + N Y.  Query rows, N
+// blocks and the row factors are loaded into registers OD chunks ahead.
+template <class CT, class IT, int DK, class OT, bool VL, bool VEC>
 __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCtx& x, int ow,
-                                              const typename Carry<CT, DK>::frag* hand) {
-  typedef Carry<CT, DK> K;
+                                              const typename Mma<CT>::frag* hand) {
+  typedef Carry<CT, IT, DK> K;
   typedef typename K::G G;
   typedef typename K::frag frag;
-  constexpr int NKX = G::NKX, NKT = G::NKT;
-  const int lane = x.lane, grp = x.grp;
+  constexpr int NKX = G::NKX, NKT = G::NKT, KB = G::KB, EPF = G::EPF, OD = K::OD, TPW = K::TPW;
+  const int lane = x.lane, grp = x.grp, col = x.col;
   struct Ops {
-    frag q[2][NKX];
-    frag nn[2][NKT];
-    float4_t eg[2];
+    frag q[TPW][NKX];
+    frag nn[TPW][NKT];
+    float4_t yo[TPW];
   };
   auto load_o = [&](Ops& o, int c) {
-    const int64_t cc = (VL ? x.c0 : 0) + min(c, x.nchunks - 1);
-    const frag* qf = static_cast<const frag*>(p.Qf) + (cc * p.Hk + x.hk) * G::NBK * 64 + lane;
-    const frag* nf = static_cast<const frag*>(p.Nf) + (cc * p.Hv + x.h) * G::NBN * 64 + lane;
-    const float* scs = p.sc + (cc * p.Hv + x.h) * 256;
+    const int cc = min(c, x.nchunks - 1);
+    int t0, n;
+    chunk_at<VL>(p, (VL ? x.c0 : 0) + cc, t0, n);
+    const int64_t cg = (VL ? x.c0 : 0) + cc;
+    const frag* nf = static_cast<const frag*>(p.Nf) + (cg * p.Hv + x.h) * G::NBN * 64 + lane;
+    const float* scs = p.sc + (cg * p.Hv + x.h) * 256;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int t = 2 * ow + tt;
+    for (int tt = 0; tt < TPW; ++tt) {
+      const int t = TPW * ow + tt;
+      const IT* qrow = static_cast<const IT*>(p.q) + (int64_t)(t0 + min(16 * t + col, n - 1)) * p.sqk +
+                       (int64_t)x.hk * p.dk;
 #pragma unroll
-      for (int kb = 0; kb < NKX; ++kb) o.q[tt][kb] = qf[(t * NKX + kb) * 64];
+      for (int kb = 0; kb < NKX; ++kb) o.q[tt][kb] = query_frag<CT, IT, VEC>(qrow, kb * KB + grp * EPF, p.dk);
 #pragma unroll
       for (int b = 0; b < NKT; ++b) o.nn[tt][b] = nf[(t * NKT + b) * 64];
-      o.eg[tt] = *reinterpret_cast<const float4_t*>(scs + 64 + 16 * t + 4 * grp);
+      o.yo[tt] = *reinterpret_cast<const float4_t*>(scs + 64 + 16 * t + 4 * grp);
     }
   };
-  Ops oa, ob;
-  load_o(oa, 0);
-  load_o(ob, 1);
+  Ops ops[OD];
+#pragma unroll
+  for (int d = 0; d < OD; ++d) load_o(ops[d], d);
   const OT* out = static_cast<const OT*>(p.out) + (int64_t)x.h * p.dv + x.j0;
-  int ooff[2][4];  // byte offsets of this lane's output rows within a chunk
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      ooff[tt][j] = x.col_ok ? ((16 * (2 * ow + tt) + 4 * grp + j) * (int)p.so + x.col) * (int)sizeof(OT) : kOOB;
+  // branch-free store offsets: columns past dv add 2^31 (past the range)
+  const uint32_t olane = (uint32_t)col * (uint32_t)sizeof(OT) + (x.col_ok ? 0u : 0x80000000u);
+  const uint32_t orow = (uint32_t)p.so * (uint32_t)sizeof(OT);
   lds_barrier();  // prologue
   lds_barrier();  // chunk 0 (no outputs yet)
   auto ostep = [&](int c, Ops& o) {
-    const frag* hs = hand + (c & 1) * K::NH * 64;
+    const frag* hs = hand + (c & 1) * (NKX + NKT) * 64;
     frag sf[NKX], yf[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKX; ++kb) sf[kb] = hs[kb * 64 + lane];
@@ -1073,32 +949,35 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
     // rows past the end of the sequence fall outside the buffer range: dropped
     const __amdgpu_buffer_rsrc_t r = make_rsrc(out + (int64_t)t0 * p.so, n * (int)p.so * (int)sizeof(OT));
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < TPW; ++tt) {
+      const int t = TPW * ow + tt;
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < NKX; ++kb) Mma<CT>::mma(acc, o.q[tt][kb], sf[kb]);
-      acc = acc * o.eg[tt];
+      acc = acc * o.yo[tt];
 #pragma unroll
       for (int b = 0; b < NKT; ++b) Mma<CT>::mma(acc, o.nn[tt][b], yf[b]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) buffer_store(r, ooff[tt][j], acc[j], OT(0));
+      for (int j = 0; j < 4; ++j)
+        buffer_store(r, (int)((uint32_t)(16 * t + 4 * grp + j) * orow + olane), acc[j], OT(0));
     }
-    load_o(o, c + 2);
+    load_o(o, c + OD);
     lds_barrier();  // end of chunk c+1
   };
   int c = 0;
-  for (; c + 1 < x.nchunks; c += 2) {
-    ostep(c, oa);
-    ostep(c + 1, ob);
-  }
-  if (c < x.nchunks) ostep(c, oa);
+  for (; c + OD <= x.nchunks; c += OD)
+#pragma unroll
+    for (int d = 0; d < OD; ++d) ostep(c + d, ops[d]);
+  for (int d = 0; c < x.nchunks; ++c, ++d) ostep(c, ops[d]);
 }
 
-template <class CT, int DK, bool VL>
-__global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
-  typedef Carry<CT, DK> K;
-  __shared__ __attribute__((aligned(16))) typename K::frag ring[K::D0 * K::SLOT];
-  __shared__ __attribute__((aligned(16))) typename K::frag hand[2 * K::NH * 64];
+// MODE 0: one sequence; 1: one sequence with a captured state; 2: a ragged batch.
+template <class CT, class IT, int DK, int MODE>
+__global__ __launch_bounds__((Carry<CT, IT, DK>::THREADS)) void scan_carry(ScanParams p) {
+  typedef Carry<CT, IT, DK> K;
+  constexpr bool VL = MODE == 2, CAP = MODE == 1;
+  __shared__ __attribute__((aligned(1024))) char ring[K::D0 * K::SLOT];
+  __shared__ __attribute__((aligned(16))) typename K::frag hand[2 * (K::G::NKX + K::G::NKT) * 64];
 
   CarryCtx x;
   x.lane = threadIdx.x & 63;
@@ -1129,7 +1008,6 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
   x.j0 = (L % ntiles) * kVT;
   x.jc = x.j0 + x.col;
   x.col_ok = x.jc < p.dv;
-  x.jcc = min(x.jc, p.dv - 1);
   x.init = p.initial ? p.initial + seq * p.init_stride : nullptr;
   x.fin = p.final_state ? p.final_state + (int64_t)seq * p.Hv * p.dk * p.dv : nullptr;
   x.cap_chunk = p.capture > 0 ? (p.capture - 1) / kC : -1;
@@ -1143,42 +1021,41 @@ __global__ __launch_bounds__(256) void scan_carry(ScanParams p) {
       }
     return;
   }
-  if (wave == 1) {
-    carry_loader<CT, DK, VL>(p, x, ring);
-  } else if (wave == 0) {
-    if constexpr (sizeof(CT) == 2) {
-      if (p.dtype_qkv == 0)
-        carry_recurrence_f16<CT, DK, float, VL>(p, x, ring, hand);
-      else
-        carry_recurrence_f16<CT, DK, half_t, VL>(p, x, ring, hand);
-    } else {
-      if (p.dtype_qkv == 0)
-        carry_recurrence<CT, DK, float, VL>(p, x, ring, hand);
-      else
-        carry_recurrence<CT, DK, half_t, VL>(p, x, ring, hand);
-    }
+  if (wave == 0) {
+    carry_recurrence<CT, IT, DK, VL, CAP>(p, x, ring, hand);
+  } else if (wave <= K::NLOAD) {
+    carry_loader<CT, IT, DK, VL>(p, x, wave, ring);
   } else {
-    if (p.dtype_out == 0)
-      carry_outputs<CT, DK, float, VL>(p, x, wave - 2, hand);
-    else
-      carry_outputs<CT, DK, half_t, VL>(p, x, wave - 2, hand);
+    const int ow = wave - 1 - K::NLOAD;
+    const bool vec = p.vec_qk && p.dk == DK;
+    if (p.dtype_out == 0) {
+      if (vec)
+        carry_outputs<CT, IT, DK, float, VL, true>(p, x, ow, hand);
+      else
+        carry_outputs<CT, IT, DK, float, VL, false>(p, x, ow, hand);
+    } else {
+      if (vec)
+        carry_outputs<CT, IT, DK, half_t, VL, true>(p, x, ow, hand);
+      else
+        carry_outputs<CT, IT, DK, half_t, VL, false>(p, x, ow, hand);
+    }
   }
 }
 
 template <class CT, class IT, int DK>
 int launch_dk(const ScanParams& p, hipStream_t stream) {
-  if (p.mixed)
-    hipLaunchKernelGGL((scan_prepare<CT, IT, DK, true>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((scan_prepare<CT, IT, DK, false>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((scan_prepare<CT, IT, DK>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
   int rc = check_launch("scan_prepare");
   if (rc) return rc;
   const int ntiles = (p.dv + kVT - 1) / kVT;
   const int nseq = p.seq_tab ? p.nseq : 1;
+  const dim3 block(Carry<CT, IT, DK>::THREADS);
   if (p.seq_tab)
-    hipLaunchKernelGGL((scan_carry<CT, DK, true>), dim3(nseq * p.Hv * ntiles), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((scan_carry<CT, IT, DK, 2>), dim3(nseq * p.Hv * ntiles), block, 0, stream, p);
+  else if (p.capture > 0)
+    hipLaunchKernelGGL((scan_carry<CT, IT, DK, 1>), dim3(p.Hv * ntiles), block, 0, stream, p);
   else
-    hipLaunchKernelGGL((scan_carry<CT, DK, false>), dim3(p.Hv * ntiles), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((scan_carry<CT, IT, DK, 0>), dim3(p.Hv * ntiles), block, 0, stream, p);
   return check_launch("scan_carry");
 }
 

@@ -124,31 +124,6 @@ int clef_delta_scan_varlen(const void* q, const void* k, const void* v, int64_t 
                            void* out, int64_t so, int dtype_out, float* final_states, void* workspace,
                            size_t workspace_bytes, void* stream);
 
-/*
- * The mixer's conv + SiLU folded into the scan (qwen.rs:603-618: projection
- * -> causal conv -> SiLU -> split -> recurrence), replacing clef_conv_silu /
- * clef_conv_silu_varlen followed by clef_delta_scan / clef_delta_scan_varlen.
- * mixed: the raw projection [T, ld_mixed] (dtype_qkv) whose first
- * 2 Hk dk + Hv dv columns are [q | k | v] (qwen.rs:731-739); conv_w: f32
- * [2 Hk dk + Hv dv][4]; history: f32 [history_rows][2 Hk dk + Hv dv] rows
- * before each sequence's first token (sequence s at history + s *
- * history_stride floats; NULL or 0 rows = zero padding).  The scan's q, k, v
- * are the conv outputs rounded to dtype_qkv, exactly as clef_conv_silu stores
- * them; the convolved v is written to v_conv ([T, Hv dv], dtype_qkv, must not
- * overlap mixed).  cu_seqlens NULL: one sequence (nseq ignored), capture as
- * clef_delta_scan; else a ragged batch as clef_delta_scan_varlen (initial +
- * s * initial_stride, no capture).  Workspace: clef_delta_scan_workspace or
- * clef_delta_scan_varlen_workspace.  taps == 4, dk == dv a multiple of 8,
- * ld_mixed a multiple of 8, mixed / conv_w / v_conv 16-byte aligned.
- */
-int clef_delta_scan_conv(const void* mixed, int64_t ld_mixed, int dtype_qkv, const float* conv_w, int taps,
-                         const float* history, int history_rows, int64_t history_stride, void* v_conv,
-                         const void* g, const void* beta, int64_t sgb, int dtype_gb, const int32_t* cu_seqlens,
-                         int nseq, int T, int Hk, int Hv, int dk, int dv, int chunk, int precision,
-                         const float* initial, int64_t initial_stride, int capture, void* out, int64_t so,
-                         int dtype_out, float* captured, float* final_states, void* workspace,
-                         size_t workspace_bytes, void* stream);
-
 /* ---------------------------------------------------------------------- */
 /* Projections                                                             */
 /* ---------------------------------------------------------------------- */
