@@ -557,24 +557,69 @@ struct Carry {
   static constexpr int SOFF = KBYTES + G::NBU * 1024;     // row scalars within a slot
   static constexpr int SLOT = SOFF + 1024;
   static constexpr int HAND = 2 * (G::NKX + G::NKT) * 1024;  // S and Y hand-off, double buffered
-  static constexpr int LDS = 160 * 1024;
-  static constexpr int OD = 2;                            // chunks of output operands in registers
-  // waves: the recurrence, NLOAD loaders, NOUT output waves of TPW 16-row tiles
-  // (f32 operands take four waves in all, so each may hold 512 registers)
+  static constexpr int LDS = 160 * 1024 - 64;             // less the exchange flags
+  // recurrence waves: f16 one (its chunk takes ~16 cycles per product; an LDS
+  // exchange of partial products between two waves costs more than it
+  // saves), f32 four (each a quarter of the products, 32 cycles each), as far
+  // as the k-blocks go and as long as two ring slots and their 4 KiB partial
+  // products still fit the LDS
+  static constexpr int rec_waves() {
+    int n = sizeof(CT) == 2 ? 1 : 4;
+    if (n > G::NKX) n = G::NKX;
+    while (n > 1 && 2 * SLOT + HAND + n * 4096 > LDS) n /= 2;
+    return n;
+  }
+  static constexpr int NREC = rec_waves();
+  static constexpr int KPR = G::NKX / NREC;               // k-blocks of the state per recurrence wave
+  static constexpr int SPR = G::NST / NREC;               // its 16-row tiles
+  static constexpr int XCH = NREC > 1 ? NREC * 4096 : 0;  // partial products Y_r
+  // waves: NREC recurrence, NLOAD loaders, NOUT output waves of TPW 16-row tiles
+  // (one f32 recurrence wave leaves room for two output waves of 512 registers)
   static constexpr int NLOAD = sizeof(CT) == 2 ? 2 : 1;
+  static constexpr int NOUT = (sizeof(CT) == 4 && NREC == 1) ? 2 : 4;
+  static constexpr int TPW = 4 / NOUT;
+  static constexpr int OD = (sizeof(CT) == 4 && NOUT == 4) ? 1 : 2;  // chunks of output operands in registers
   // ring slots: at most 4, as many as the LDS holds, and few enough that the
   // DMA instructions a loader keeps in flight fit the 6-bit vmcnt
   static constexpr int PERW = NLOAD == 1 ? NDK + G::NBU + 1 : (NDK > G::NBU + 1 ? NDK : G::NBU + 1);
-  static constexpr int DL = (LDS - HAND) / SLOT, DV = 2 + 63 / PERW;
+  static constexpr int DL = (LDS - HAND - XCH) / SLOT, DV = 2 + 63 / PERW;
   static constexpr int D0 = DL < DV ? (DL < 4 ? DL : 4) : (DV < 4 ? DV : 4);
-  static constexpr int NOUT = sizeof(CT) == 2 ? 4 : 2;
-  static constexpr int TPW = 4 / NOUT;
-  static constexpr int THREADS = 64 * (1 + NLOAD + NOUT);
-  static_assert(D0 >= 2 && D0 * SLOT + HAND <= LDS, "two ring slots fit the LDS");
+  static constexpr int THREADS = 64 * (NREC + NLOAD + NOUT);
+  // with three or more slots the loaders land chunk i+1 before chunk i
+  // starts, so the recurrence reads the next chunk's keys during this one
+  // (not with f32 keys under f16 products: their conversion needs the room)
+  static constexpr bool PREF = D0 >= 3 && sizeof(IT) == sizeof(CT);
+  static_assert(D0 >= 2 && D0 * SLOT + HAND + XCH <= LDS, "two ring slots fit the LDS");
+  static_assert(G::NKX % NREC == 0 && G::NST % NREC == 0, "whole k-blocks per recurrence wave");
   static_assert(NLOAD == 2 ? (D0 - 2) * NDK < 64 && (D0 - 2) * (G::NBU + 1) < 64
                            : (D0 - 2) * (NDK + G::NBU + 1) < 64, "ring wait counts fit vmcnt");
   static_assert(KBYTES % 1024 == 0, "whole DMA instructions per chunk of keys");
 };
+
+// LDS hand-off between the recurrence waves of a work-group: wave r sets byte
+// r of one flag word to the chunk count mod 256 once its partial product is
+// in LDS (the waves are never a whole chunk apart: they meet at the barrier
+// that ends each chunk), and a single read of the word sees every wave.  The
+// word is accessed through an LDS-space pointer: a volatile access through a
+// generic pointer becomes a system-coherent flat access that waits for every
+// outstanding global load.
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef __attribute__((address_space(3))) unsigned lds_u32;
+// Every earlier LDS access of the wave has completed before its byte changes.
+__device__ __forceinline__ void lds_publish(unsigned* flags, int r, unsigned v) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  *((volatile lds_u8*)flags + r) = (unsigned char)v;
+}
+// Waits until the low n bytes of the word all read v.  Bounded: after 2^22
+// polls the wave goes on, so every wave reaches the end of the kernel.
+__device__ __forceinline__ void lds_wait_all(const unsigned* flags, int n, unsigned v) {
+  const unsigned mask = n >= 4 ? 0xffffffffu : (1u << (8 * n)) - 1u;
+  const unsigned want = (v & 0xffu) * 0x01010101u & mask;
+  const volatile lds_u32* f = (const volatile lds_u32*)flags;
+  for (int k = 0; k < (1 << 22); ++k)
+    if ((*f & mask) == want) break;
+  asm volatile("" ::: "memory");
+}
 
 struct CarryCtx {
   int h, hk, j0, jc;
@@ -696,10 +741,10 @@ __device__ __forceinline__ void carry_ublocks(const ScanParams& p, const CarryCt
 }
 
 template <class CT, class IT, int DK, bool VL>
-__device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x, int wave, char* ring) {
+__device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x, int lw, char* ring) {
   typedef Carry<CT, IT, DK> K;
   const bool fast = p.vec_qk && p.dk == DK;
-  const bool keys = K::NLOAD == 1 || wave == 1, ublocks = K::NLOAD == 1 || wave == 2;
+  const bool keys = K::NLOAD == 1 || lw == 0, ublocks = K::NLOAD == 1 || lw == 1;
   // outstanding DMA instructions per chunk for this wave (fast key path)
   constexpr int PER = K::NLOAD == 1 ? K::NDK + K::G::NBU + 1 : 0;
   auto slot = [&](int c) { return ring + (c % K::D0) * K::SLOT; };
@@ -715,13 +760,14 @@ __device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx
   for (int i = 0; i < x.nchunks; ++i) {
     if (i + K::D0 - 1 < x.nchunks) {
       issue(i + K::D0 - 1);
-      // chunk i+1 has landed
+      // chunk i+1 (prefetching recurrence: i+2) has landed
+      constexpr int AHEAD = K::D0 - 2 - (K::PREF ? 1 : 0);
       if constexpr (K::NLOAD == 1)
-        wait_vmcnt<(K::D0 - 2) * PER>();
-      else if (wave == 1)
-        wait_vmcnt<(K::D0 - 2) * K::NDK>();
+        wait_vmcnt<AHEAD * PER>();
+      else if (lw == 0)
+        wait_vmcnt<AHEAD * K::NDK>();
       else
-        wait_vmcnt<(K::D0 - 2) * (K::G::NBU + 1)>();
+        wait_vmcnt<AHEAD * (K::G::NBU + 1)>();
     } else {
       wait_vmcnt<0>();
     }
@@ -731,43 +777,47 @@ __device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx
   lds_barrier();  // outputs of the last chunk
 }
 
-// Wave 0: the recurrence.  Per chunk i (slot i % D0):
-//   X = K S (raw keys, rows in slot order), Y = V - (a e^gam) X,
-//   S <- e^gam_last S + U Y;
-// S_i and Y_i go to the output waves through `hand`.
-template <class CT, class IT, int DK, bool VL, bool CAP>
+// Recurrence wave R of NREC: it holds the KPR k-blocks KB0 = R KPR.. of the
+// state (its 16-row tiles S0 = R SPR..).  Per chunk i (slot i % D0):
+//   X_R = K_R S_R (raw key columns of those k-blocks),
+//   P_R = -(a e^gam) X_R, plus V in wave 0 (beta is folded into U and N),
+//   Y = P_0 + P_1 + ... (exchanged in LDS, summed in the same order by all),
+//   S_R <- e^gam_last S_R + U_R Y (the wave's rows of U).
+// With one wave this is Y = V - (a e^gam) K S.  S_i and Y_i go to the output
+// waves through `hand`.
+template <class CT, class IT, int DK, bool VL, bool CAP, int R>
 __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const CarryCtx& x, const char* ring,
-                                                 typename Mma<CT>::frag* hand) {
+                                                 typename Mma<CT>::frag* hand, float4_t* xch, unsigned* xflag) {
   typedef Carry<CT, IT, DK> K;
   typedef typename K::G G;
   typedef typename K::frag frag;
-  constexpr int NST = G::NST, NKX = G::NKX, NKT = G::NKT, NBU = G::NBU, TPK = G::TPK, KB = G::KB;
-  constexpr int EPF = G::EPF;
+  constexpr int NKX = G::NKX, NKT = G::NKT, NBU = G::NBU, KB = G::KB, EPF = G::EPF;
+  constexpr int NREC = K::NREC, KPR = K::KPR, SPR = K::SPR, KB0 = R * KPR, S0 = R * SPR;
   const int lane = x.lane, grp = x.grp, col = x.col;
   const int dk = p.dk, dv = p.dv;
   const float* init = VL ? x.init : p.initial;
   float* fin = VL ? x.fin : p.final_state;
 
-  float4_t S[NST];
+  float4_t S[SPR];
 #pragma unroll
-  for (int s = 0; s < NST; ++s)
+  for (int s = 0; s < SPR; ++s)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = slot_index<CT>(s, 4 * grp + i);
+      const int row = slot_index<CT>(S0 + s, 4 * grp + i);
       float v = 0.0f;
       if (init && row < dk && x.col_ok) v = init[((int64_t)x.h * dk + row) * dv + x.jc];
       S[s][i] = v;
     }
-  frag Sf[NKX];
+  frag Sf[KPR];
 #pragma unroll
-  for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
+  for (int k = 0; k < KPR; ++k) Sf[k] = pack_frag(S, k, CT(0));
 
-  // v two chunks ahead in registers (this lane's 16 X-rows); rows past the
-  // end of the sequence fall outside the buffer range (read 0), and so do
-  // columns past dv: their lanes add 2^31 to every offset (a chunk's range
-  // is at most 64 rows of 2^22 four-byte elements, 2^30 bytes, so the sum
-  // stays in 32 bits and past the range).  Branch-free offsets keep the loads
-  // unconditional, so they stay in flight across the loop.
+  // wave 0: v two chunks ahead in registers (this lane's 16 X-rows); rows
+  // past the end of the sequence fall outside the buffer range (read 0), and
+  // so do columns past dv: their lanes add 2^31 to every offset (a chunk's
+  // range is at most 64 rows of 2^22 four-byte elements, 2^30 bytes, so the
+  // sum stays in 32 bits and past the range).  Branch-free offsets keep the
+  // loads unconditional, so they stay in flight across the loop.
   const IT* vbase = static_cast<const IT*>(p.v) + (int64_t)x.h * dv + x.j0;
   const uint32_t vlane = (uint32_t)col * (uint32_t)sizeof(IT) + (x.col_ok ? 0u : 0x80000000u);
   const uint32_t vrow = (uint32_t)p.sv * (uint32_t)sizeof(IT);
@@ -781,97 +831,150 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
       for (int j = 0; j < 4; ++j)
         vb[4 * t + j] = buffer_load_bits<IT>(r, (int)((uint32_t)slot_index<CT>(t, 4 * grp + j) * vrow + vlane));
   };
-  uint32_t va[16], vb[16];
-  load_v(va, 0);
-  load_v(vb, 1);
+  constexpr int NV = R == 0 ? 16 : 1;
+  uint32_t va[NV], vb[NV];
+  if constexpr (R == 0) {
+    load_v(va, 0);
+    load_v(vb, 1);
+  }
   // this lane's key rows (slot order) and k offset within each k-block
   int krow[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) krow[t] = slot_index<CT>(t, col);
+  frag kf[4][KPR];
+  auto load_k = [&](int c) {
+    const char* slot = ring + (c % K::D0) * K::SLOT;
+#pragma unroll
+    for (int k = 0; k < KPR; ++k)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) kf[t][k] = key_frag<CT, IT, DK>(slot, krow[t], (KB0 + k) * KB + grp * EPF);
+  };
   lds_barrier();  // prologue
+  if constexpr (K::PREF) load_k(0);
 
   auto step = [&](int i, uint32_t* vbuf) {
     const char* slot = ring + (i % K::D0) * K::SLOT;
     const frag* uslot = reinterpret_cast<const frag*>(slot + K::UOFF);
     const float* scs = reinterpret_cast<const float*>(slot + K::SOFF);  // a e^gam, b e^gam, gam, e^gam
     frag* hs = hand + (i & 1) * (NKX + NKT) * 64;
-    frag kf[4][NKX];
+    // the chunk's keys: read during the previous chunk, or up front
+    if constexpr (!K::PREF) load_k(i);
     float4_t ya[4], X[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) kf[t][0] = key_frag<CT, IT, DK>(slot, krow[t], grp * EPF);
+    for (int t = 0; t < 4; ++t) ya[t] = *reinterpret_cast<const float4_t*>(scs + slot_index<CT>(t, 4 * grp));
+    // the wave's U rows: into the key registers once the last product has
+    // taken its operands (f32, four recurrence waves: after its partial
+    // product is published, for want of registers)
+    constexpr bool EARLY_U = NREC <= 2;
+    frag uf[SPR][NKT];
+    auto load_u = [&]() {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < SPR; ++s)
+#pragma unroll
+        for (int b = 0; b < NKT; ++b) uf[s][b] = uslot[((S0 + s) * NKT + b) * 64 + lane];
+    };
+    const float el = scs[192 + kC - 1];
     // S_i goes to the output waves
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) hs[kb * 64 + lane] = Sf[kb];
+    for (int k = 0; k < KPR; ++k) hs[(KB0 + k) * 64 + lane] = Sf[k];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) X[t] = float4_t{0.f, 0.f, 0.f, 0.f};
     __builtin_amdgcn_sched_barrier(0);
-    // X = K S in rounds of 4 independent products; each round also requests
-    // the next round's operands
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) {
-      if (kb + 1 < NKX) {
+    for (int k = 0; k < KPR; ++k) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) kf[t][kb + 1] = key_frag<CT, IT, DK>(slot, krow[t], (kb + 1) * KB + grp * EPF);
-      }
-      if (kb == 0) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) ya[t] = *reinterpret_cast<const float4_t*>(scs + slot_index<CT>(t, 4 * grp));
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kf[t][kb], Sf[kb]);
+      for (int t = 0; t < 4; ++t) Mma<CT>::mma(X[t], kf[t][k], Sf[k]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    const float el = scs[192 + kC - 1];
-    frag uf[NST][NKT];
+    if constexpr (EARLY_U) {
+      load_u();
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-    for (int s = 0; s < NST; ++s)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int b = 0; b < NKT; ++b) uf[s][b] = uslot[(s * NKT + b) * 64 + lane];
-    // Y = V - (a e^gam) X for token block b (beta is folded into U and N)
-    frag Yf[NKT];
-    auto y_block = [&](int b) {
-#pragma unroll
-      for (int u = 0; u < TPK; ++u) {
-        const int t = TPK * b + u;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) X[t][j] = bits_value<IT>(vbuf[4 * t + j]) - ya[t][j] * X[t][j];
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (R == 0)
+          X[t][j] = bits_value<IT>(vbuf[4 * t + j]) - ya[t][j] * X[t][j];
+        else
+          X[t][j] = -(ya[t][j] * X[t][j]);
       }
-      Yf[b] = pack_frag(X, b, CT(0));
-    };
+    if constexpr (NREC > 1) {
+      float4_t* mine = xch + R * 4 * 64;
 #pragma unroll
-    for (int b = 0; b < NKT; ++b) y_block(b);
+      for (int t = 0; t < 4; ++t) mine[t * 64 + lane] = X[t];
+      lds_publish(xflag, R, i + 1);
+      if constexpr (!EARLY_U) load_u();
+      lds_wait_all(xflag, NREC, i + 1);
+      if constexpr (EARLY_U) {
+        // the other waves' partials, all requested before the first sum
+        float4_t px[NREC][4];
+#pragma unroll
+        for (int r = 0; r < NREC; ++r)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) px[r][t] = r == R ? X[t] : xch[(r * 4 + t) * 64 + lane];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float4_t acc = px[0][t];
+#pragma unroll
+          for (int r = 1; r < NREC; ++r) acc = acc + px[r][t];
+          X[t] = acc;
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float4_t acc = R == 0 ? X[t] : xch[t * 64 + lane];
+#pragma unroll
+          for (int r = 1; r < NREC; ++r) acc = acc + (r == R ? X[t] : xch[(r * 4 + t) * 64 + lane]);
+          X[t] = acc;
+        }
+      }
+    }
+    frag Yf[NKT];
+#pragma unroll
+    for (int b = 0; b < NKT; ++b) Yf[b] = pack_frag(X, b, CT(0));
     if (CAP && i == x.cap_chunk) {
       // state after token `capture`: exp(gam_r*) S_i + Ucap Y_i
       const float ec = decay_exp(scs[128 + x.cap_row]);
       const frag* uc = static_cast<const frag*>(p.Ucf) + (int64_t)x.h * NBU * 64 + lane;
 #pragma unroll
-      for (int s = 0; s < NST; ++s) {
+      for (int s = 0; s < SPR; ++s) {
         float4_t acc = S[s] * ec;
 #pragma unroll
-        for (int b = 0; b < NKT; ++b) Mma<CT>::mma(acc, uc[(s * NKT + b) * 64], Yf[b]);
+        for (int b = 0; b < NKT; ++b) Mma<CT>::mma(acc, uc[((S0 + s) * NKT + b) * 64], Yf[b]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int row = slot_index<CT>(s, 4 * grp + j);
+          const int row = slot_index<CT>(S0 + s, 4 * grp + j);
           if (row < dk && x.col_ok) p.captured[((int64_t)x.h * dk + row) * dv + x.jc] = acc[j];
         }
       }
     }
     // Y_i goes to the output waves
+    if constexpr (R == 0) {
 #pragma unroll
-    for (int b = 0; b < NKT; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
+      for (int b = 0; b < NKT; ++b) hs[(NKX + b) * 64 + lane] = Yf[b];
+    }
     __builtin_amdgcn_sched_barrier(0);
-    // S <- exp(gam_last) S + U Y
+    // S <- exp(gam_last) S + U Y: each tile's rescale is issued while the
+    // previous tile's product runs, and the next chunk's keys are requested
+    // once the U operands are in
 #pragma unroll
-    for (int s = 0; s < NST; ++s) S[s] = S[s] * el;
+    for (int s = 0; s < SPR; ++s) {
+      S[s] = S[s] * el;
+      Mma<CT>::mma(S[s], uf[s][0], Yf[0]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int b = 0; b < NKT; ++b) {
+    for (int b = 1; b < NKT; ++b) {
 #pragma unroll
-      for (int s = 0; s < NST; ++s) Mma<CT>::mma(S[s], uf[s][b], Yf[b]);
+      for (int s = 0; s < SPR; ++s) Mma<CT>::mma(S[s], uf[s][b], Yf[b]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (K::PREF) load_k(i + 1);
 #pragma unroll
-    for (int kb = 0; kb < NKX; ++kb) Sf[kb] = pack_frag(S, kb, CT(0));
-    load_v(vbuf, i + 2);
+    for (int k = 0; k < KPR; ++k) Sf[k] = pack_frag(S, k, CT(0));
+    if constexpr (R == 0) load_v(vbuf, i + 2);
     lds_barrier();  // end of chunk i
   };
   int i = 0;
@@ -884,10 +987,10 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
 
   if (fin) {
 #pragma unroll
-    for (int s = 0; s < NST; ++s)
+    for (int s = 0; s < SPR; ++s)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int row = slot_index<CT>(s, 4 * grp + j);
+        const int row = slot_index<CT>(S0 + s, 4 * grp + j);
         if (row < dk && x.col_ok) fin[((int64_t)x.h * dk + row) * dv + x.jc] = S[s][j];
       }
   }
@@ -968,7 +1071,10 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
   for (; c + OD <= x.nchunks; c += OD)
 #pragma unroll
     for (int d = 0; d < OD; ++d) ostep(c + d, ops[d]);
-  for (int d = 0; c < x.nchunks; ++c, ++d) ostep(c, ops[d]);
+  // the last chunks; compile-time indices keep ops in registers
+#pragma unroll
+  for (int d = 0; d + 1 < OD; ++d)
+    if (c + d < x.nchunks) ostep(c + d, ops[d]);
 }
 
 // MODE 0: one sequence; 1: one sequence with a captured state; 2: a ragged batch.
@@ -978,6 +1084,9 @@ __global__ __launch_bounds__((Carry<CT, IT, DK>::THREADS)) void scan_carry(ScanP
   constexpr bool VL = MODE == 2, CAP = MODE == 1;
   __shared__ __attribute__((aligned(1024))) char ring[K::D0 * K::SLOT];
   __shared__ __attribute__((aligned(16))) typename K::frag hand[2 * (K::G::NKX + K::G::NKT) * 64];
+  __shared__ __attribute__((aligned(16))) float4_t xch[K::NREC > 1 ? K::NREC * 4 * 64 : 1];
+  __shared__ unsigned xflag[1];
+  if (threadIdx.x == 0) xflag[0] = 0;  // before the prologue barrier
 
   CarryCtx x;
   x.lane = threadIdx.x & 63;
@@ -1021,12 +1130,19 @@ __global__ __launch_bounds__((Carry<CT, IT, DK>::THREADS)) void scan_carry(ScanP
       }
     return;
   }
-  if (wave == 0) {
-    carry_recurrence<CT, IT, DK, VL, CAP>(p, x, ring, hand);
-  } else if (wave <= K::NLOAD) {
-    carry_loader<CT, IT, DK, VL>(p, x, wave, ring);
+  if (wave < K::NREC) {
+    if (wave == 0) carry_recurrence<CT, IT, DK, VL, CAP, 0>(p, x, ring, hand, xch, xflag);
+    if constexpr (K::NREC > 1) {
+      if (wave == 1) carry_recurrence<CT, IT, DK, VL, CAP, 1>(p, x, ring, hand, xch, xflag);
+    }
+    if constexpr (K::NREC > 2) {
+      if (wave == 2) carry_recurrence<CT, IT, DK, VL, CAP, 2>(p, x, ring, hand, xch, xflag);
+      if (wave == 3) carry_recurrence<CT, IT, DK, VL, CAP, 3>(p, x, ring, hand, xch, xflag);
+    }
+  } else if (wave < K::NREC + K::NLOAD) {
+    carry_loader<CT, IT, DK, VL>(p, x, wave - K::NREC, ring);
   } else {
-    const int ow = wave - 1 - K::NLOAD;
+    const int ow = wave - K::NREC - K::NLOAD;
     const bool vec = p.vec_qk && p.dk == DK;
     if (p.dtype_out == 0) {
       if (vec)
