@@ -59,9 +59,6 @@ SIGNATURES = {
     "clef_rms_norm": (_i, [_p, _l, _i, _p, _p, _l, _i, _i, _i, _f, _p]),
     "clef_conv_silu": (_i, [_p, _l, _i, _p, _i, _p, _i, _p, _l, _i, _i, _i, _p]),
     "clef_delta_gates": (_i, [_p, _l, _p, _l, _i, _p, _p, _p, _p, _i, _i, _p]),
-    "clef_gemm_pack_bytes": (_z, [_i, _i]),
-    "clef_gemm_pack": (_i, [_p, _l, _i, _i, _i, _p, _p]),
-    "clef_gemm_packed": (_i, [_p, _l, _p, _z, _p, _l, _i, _i, _i, _i, _i, _i, _p]),
     "clef_delta_gates_pack_bytes": (_z, [_i, _i]),
     "clef_delta_gates_pack": (_i, [_p, _l, _i, _i, _i, _p, _p]),
     "clef_delta_gates_proj": (_i, [_p, _l, _p, _i, _i, _p, _p, _p, _p, _i, _i, _p]),
@@ -288,36 +285,6 @@ def gemm_swiglu(x, wg, wu, out=None):
     y = out if out is not None else torch.empty((M, N), dtype=x.dtype, device=x.device)
     _check(lib().clef_gemm_swiglu(_ptr(x), _rows(x, "x"), _ptr(wg), _ptr(wu), _rows(wg, "wg"),
                                   _ptr(y), _rows(y, "y"), M, N, K, _dt(x), _stream()))
-    return y
-
-
-class PackedWeights:
-    """A projection's f16 weights packed once in fragment order (clef_gemm_pack)."""
-
-    def __init__(self, w):
-        N, K = w.shape
-        if w.dtype != torch.float16:
-            raise ClefError(-1, "packed weights: f16 [N, K]")
-        n = lib().clef_gemm_pack_bytes(N, K)
-        if n == 0:
-            raise ClefError(-1, "packed weights: K must be a multiple of 64")
-        self.buffer = torch.empty(n, dtype=torch.uint8, device=w.device)
-        self.N, self.K = N, K
-        _check(lib().clef_gemm_pack(_ptr(w), _rows(w, "w"), N, K, _dt(w), _ptr(self.buffer), _stream()))
-
-
-def gemm_packed(x, pw: PackedWeights, out=None, out_dtype=None, residual=None):
-    """gemm over packed weights (store or residual epilogue)."""
-    M, K = x.shape
-    if K != pw.K:
-        raise ClefError(-1, "GEMM operand shapes")
-    if residual is not None:
-        y, epi, dto = residual, EPI_RESIDUAL, _DT[out_dtype or x.dtype]
-    else:
-        y = out if out is not None else torch.empty((M, pw.N), dtype=out_dtype or x.dtype, device=x.device)
-        epi, dto = EPI_STORE, _dt(y)
-    _check(lib().clef_gemm_packed(_ptr(x), _rows(x, "x"), _ptr(pw.buffer), pw.buffer.numel(), _ptr(y),
-                                  _rows(y, "y"), M, pw.N, K, _dt(x), dto, epi, _stream()))
     return y
 
 

@@ -50,40 +50,6 @@ extern "C" int clef_gemm_swiglu(const void* x, int64_t ldx, const void* wg, cons
   return clef::gemm_launch(p, 2, static_cast<hipStream_t>(stream));
 }
 
-extern "C" size_t clef_gemm_pack_bytes(int N, int K) {
-  if (N < 1 || N > (1 << 20) || K < 64 || K % 64 != 0 || K > (1 << 20)) return 0;
-  return clef::gemm_pack_f16_bytes(N, K);
-}
-
-extern "C" int clef_gemm_pack(const void* w, int64_t ldw, int N, int K, int dtype, void* packed, void* stream) {
-  if (ldw == 0) ldw = K;
-  CLEF_REQUIRE(w && packed, "GEMM pack: null pointer");
-  CLEF_REQUIRE(dtype == CLEF_F16, "GEMM pack: f16 weights only");
-  CLEF_REQUIRE(N >= 1 && N <= (1 << 20) && K >= 64 && K % 64 == 0 && K <= (1 << 20) && ldw >= K,
-               "GEMM pack: dimensions (K a multiple of 64)");
-  CLEF_REQUIRE(vec_ok(w, ldw, w, ldw, nullptr, K, dtype) && (reinterpret_cast<uintptr_t>(packed) & 15) == 0,
-               "GEMM pack: rows must be 16-byte aligned");
-  return clef::gemm_pack_f16_launch(w, ldw, N, K, packed, static_cast<hipStream_t>(stream));
-}
-
-extern "C" int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, size_t packed_bytes, void* y,
-                                int64_t ldy, int M, int N, int K, int dtype_in, int dtype_out, int epilogue,
-                                void* stream) {
-  if (ldx == 0) ldx = K;
-  if (ldy == 0) ldy = N;
-  if (int rc = gemm_checks(x, ldx, packed, K, nullptr, y, ldy, M, N, K, dtype_in, dtype_out)) return rc;
-  CLEF_REQUIRE(dtype_in == CLEF_F16, "GEMM (packed): f16 operands only");
-  // every packed-weight read then stays inside the buffer
-  CLEF_REQUIRE(packed_bytes != 0 && packed_bytes == clef_gemm_pack_bytes(N, K),
-               "GEMM (packed): packed_bytes does not match clef_gemm_pack_bytes(N, K)");
-  CLEF_REQUIRE(epilogue == CLEF_EPI_STORE || epilogue == CLEF_EPI_RESIDUAL,
-               "GEMM (packed): store or residual epilogue (SwiGLU: clef_gemm_swiglu)");
-  CLEF_REQUIRE(K % 64 == 0 && vec_ok(x, ldx, packed, K, nullptr, K, dtype_in) && (int64_t)M * ldx < (int64_t(1) << 31),
-               "GEMM (packed): K a multiple of 64, 16-byte aligned rows");
-  clef::GemmParams p{x, packed, nullptr, y, ldx, K, ldy, M, N, K, dtype_in, dtype_out, 1};
-  return clef::gemm_f16_pk_launch(p, epilogue, static_cast<hipStream_t>(stream));
-}
-
 static int gates_proj_dims(int K, int Hv) {
   CLEF_REQUIRE(K >= 256 && K % 256 == 0 && K <= 4096 && (Hv == 16 || Hv == 32 || Hv == 64),
                "gates projection: K must be a multiple of 256 up to 4096 and Hv 16, 32 or 64");

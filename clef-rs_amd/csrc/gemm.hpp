@@ -25,12 +25,6 @@ bool gemm_f16_dma_ok(const GemmParams& p);
 int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t stream);
 int gemm_f16_tile_width(const GemmParams& p, int epilogue);  // 256, 192 or 128
 
-// f16 path with weights pre-packed in fragment order (gemm_f16_pk.hip);
-// p.w is the packed buffer, K % 64 == 0, x rows 16-byte aligned
-size_t gemm_pack_f16_bytes(int N, int K);
-int gemm_pack_f16_launch(const void* w, int64_t ldw, int N, int K, void* packed, hipStream_t stream);
-int gemm_f16_pk_launch(const GemmParams& p, int epilogue, hipStream_t stream);
-
 // a/b projections fused with the DeltaNet gates (gemm_f16.hip); f16 operands,
 // Hv in {16, 32, 64}, K % 256 == 0, K <= 4096, rows 16-byte aligned (checked
 // by the caller).  The weights are first packed into MFMA fragment order.

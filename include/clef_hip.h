@@ -74,8 +74,8 @@ int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, in
  * address is looked up once per device, at the first call with that device
  * current; the stream must belong to the current device).  A shape whose
  * clef_delta_scan_workspace exceeds it is rejected before any launch (the
- * full layer shape T = 4096, Hk = 16, Hv = 32, dk = dv = 128 needs 82.5 MiB in
- * the mixed profile).  Arguments and results as clef_delta_scan.  Every call
+ * full layer shape T = 4096, Hk = 16, Hv = 32, dk = dv = 128 needs 50.5 MiB in
+ * the mixed profile and 99 MiB, which is refused, in the strict one).  Arguments and results as clef_delta_scan.  Every call
  * on a GPU uses that GPU's one array: calls that overlap in time on one GPU
  * (other streams, other threads) race, and the caller must serialize them.
  */
@@ -151,25 +151,6 @@ int clef_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
  */
 int clef_gemm_swiglu(const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
                      void* y, int64_t ldy, int M, int N, int K, int dtype, void* stream);
-/*
- * The same projections with the weights packed once (f16 only): a loader
- * that owns its weights packs each projection into MFMA fragment order
- * (clef_gemm_pack, into clef_gemm_pack_bytes(N, K) bytes of device memory,
- * 16-byte aligned), and the packed GEMM then reads every weight fragment as
- * consecutive bytes straight into registers, leaving the LDS to the
- * activations.  K must be a multiple of 64.  clef_gemm_packed: as clef_gemm,
- * epilogues CLEF_EPI_STORE and CLEF_EPI_RESIDUAL with the same roundings
- * (SwiGLU: clef_gemm_swiglu); packed_bytes is the size of the packed buffer
- * and must equal clef_gemm_pack_bytes(N, K), so every weight read stays
- * inside the buffer (a buffer of another size is rejected before launch).
- * Extends the reference's GemmKernel
- * (neural.rs:50-58), whose weights stay row-major; clef_gemm remains the
- * drop-in entry point.
- */
-size_t clef_gemm_pack_bytes(int N, int K);
-int clef_gemm_pack(const void* w, int64_t ldw, int N, int K, int dtype, void* packed, void* stream);
-int clef_gemm_packed(const void* x, int64_t ldx, const void* packed, size_t packed_bytes, void* y, int64_t ldy,
-                     int M, int N, int K, int dtype_in, int dtype_out, int epilogue, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Pointwise pieces around the scan                                        */

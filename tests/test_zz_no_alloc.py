@@ -71,7 +71,7 @@ def test_noalloc_scan_equals_workspace_scan(clef, precision):
 
 @gpu
 def test_noalloc_scan_rejects_shapes_above_the_array(clef):
-    """The strict workspace of the full layer shape (163 MiB) exceeds the
+    """The strict workspace of the full layer shape (99 MiB) exceeds the
     96 MiB array: refused before any launch, and the next call still works."""
     T, Hk, Hv, dk, dv = 4096, 16, 32, 128, 128
     assert clef.lib().clef_delta_scan_workspace(T, Hk, Hv, dk, dv, 64, clef.STRICT) > 96 << 20
