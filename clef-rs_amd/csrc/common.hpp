@@ -63,6 +63,29 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// Sum over each row of 16 lanes with DPP moves (no LDS round trips): lane
+// partners xor 1 and xor 2 (quad permutes), then the half-row and row
+// mirrors, which pair the same quads and halves as xor 4 and xor 8.  Each
+// step adds a value to its partner's, so every lane of a row ends with the
+// same bits, summed in the association of an xor butterfly.
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// The same over groups of N = 2, 4, 8, 16 or 32 consecutive lanes (32: the
+// two rows meet through one lane shuffle).
+template <int N>
+__device__ __forceinline__ float lane_sum(float v) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "2..32 lanes");
+  if constexpr (N >= 2) v += dpp_partner<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) v += dpp_partner<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) v += dpp_partner<0x141>(v);  // row_half_mirror
+  if constexpr (N >= 16) v += dpp_partner<0x140>(v);  // row_mirror
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+__device__ __forceinline__ float sum16(float v) { return lane_sum<16>(v); }
+
 // Work-group barrier for LDS producer/consumer hand-offs only.  Unlike
 // __syncthreads() it does not wait for outstanding global loads, so register
 // prefetches issued before it stay in flight across the barrier.

@@ -218,18 +218,19 @@ __device__ __forceinline__ float l2norm_row(const float* x, float extra, CT* dst
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < VI; ++i) s = fmaf(x[i], x[i], s);
-#pragma unroll
-  for (int off = 1; off < TPR; off <<= 1) s += __shfl_xor(s, off, 64);
+  s = lane_sum<TPR>(s);  // DPP moves, the association of an xor butterfly
   const float inv = 1.0f / sqrtf(s + 1e-6f);
   const float scale = inv * extra;
+  CT out[VI];
 #pragma unroll
   for (int i = 0; i < VI; ++i) {
     const float v = x[i] * scale;
     if constexpr (sizeof(CT) == 2)
-      dst[i] = to_f16(v);
+      out[i] = to_f16(v);
     else
-      dst[i] = v;
+      out[i] = v;
   }
+  __builtin_memcpy(dst, out, sizeof(out));  // one vector store (dst is 16-byte aligned)
   return scale;
 }
 
@@ -353,6 +354,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   // ---- 3. per v-head
   for (int v = 0; v < rep; ++v) {
     const int h = hk * rep + v;
+    uint32_t gnext = 0, bnext = 0;
     const int64_t cv = (int64_t)chunk * p.Hv + h;
     // 3a. cumulative decay and the per-row factors (wave 0, lane = token):
     //     the carry's row factors 1/|k| e^gam (for V - e^gam K^ S) and
@@ -360,10 +362,10 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     if (wave == 0) {
       const float gv = lane < n ? bits_to_f32(gbits, p.dtype_gb) : 0.0f;
       const float bv = lane < n ? bits_to_f32(bbits, p.dtype_gb) : 0.0f;
-      if (v + 1 < rep) {  // next v-head's g and beta
+      if (v + 1 < rep) {  // next v-head's g and beta, awaited at the end of this one
         const int64_t gi = (int64_t)(t0 + min(lane, n - 1)) * p.sgb + h + 1;
-        gbits = load_bits(p.g, gi, p.dtype_gb);
-        bbits = load_bits(p.beta, gi, p.dtype_gb);
+        gnext = load_bits(p.g, gi, p.dtype_gb);
+        bnext = load_bits(p.beta, gi, p.dtype_gb);
       }
       float cs = gv;
 #pragma unroll
@@ -395,14 +397,20 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
       const int tc = idx - tr * (tr + 1) / 2;
       const int c = 16 * tc + col;
       const float gc = sGam[c];
+      // the four rows' gam and beta as vectors; the ratio is exponentiated for
+      // every element and masked afterwards (above the diagonal it may be
+      // inf, and the select keeps it out), so the block has no branches
+      const float4_t gr = *reinterpret_cast<const float4_t*>(sGam + 16 * tr + 4 * grp);
+      const float4_t br = *reinterpret_cast<const float4_t*>(sBeta + 16 * tr + 4 * grp);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * tr + 4 * grp + i;
-        const float d = (c <= r) ? decay_exp(sGam[r] - gc) : 0.0f;
+        const float e = decay_exp(gr[i] - gc);
+        const float d = c <= r ? e : 0.0f;
         if (!isqk)
-          sA[r * LDF + c] = (c < r) ? (sBeta[r] * gram[s][i]) * d : 0.0f;
+          sA[r * LDF + c] = c < r ? (br[i] * gram[s][i]) * d : 0.0f;
         else
-          sM[r * LDT + c] = static_cast<CT>((c <= r) ? gram[s][i] * d : 0.0f);
+          sM[r * LDT + c] = static_cast<CT>(c <= r ? gram[s][i] * d : 0.0f);
       }
     }
     lds_barrier();
@@ -506,6 +514,8 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
         dst[(t * NKT + b) * 64 + lane] = pack_frag(acc, 0, CT(0));
       }
     }
+    gbits = gnext;  // the loads were issued a whole v-head ago
+    bbits = bnext;
     lds_barrier();  // before the next v-head rewrites sA, sTT, sM, sGam
   }
 

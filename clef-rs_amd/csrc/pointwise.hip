@@ -380,23 +380,6 @@ __global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restri
 // reciprocal (silu_hw) instead of expf and an IEEE division.
 constexpr int kGatedRows = 1;
 
-// Sum over each row of 16 lanes with DPP moves (no LDS round trips): lane
-// partners xor 1 and xor 2 (quad permutes), then the half-row and row
-// mirrors, which pair the same quads and halves as xor 4 and xor 8.  Each
-// step adds a value to its partner's, so every lane of a row ends with the
-// same bits, summed in the association of an xor butterfly.
-template <int CTRL>
-__device__ __forceinline__ float dpp_partner(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float sum16(float v) {
-  v += dpp_partner<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_partner<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_partner<0x141>(v);  // row_half_mirror
-  v += dpp_partner<0x140>(v);  // row_mirror
-  return v;
-}
-
 template <class T8>
 __device__ __forceinline__ void load8_f32(const T8* src, float* v) {
   if constexpr (sizeof(T8) == 2) {
