@@ -77,25 +77,53 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   }
 
   const int key_end = min(p.kn, offset + q0 + BQ);  // exclusive causal limit of this group
-  for (int j0 = 0; j0 < key_end; j0 += BKEY) {
-    // ---- stage K [64][D] and V^T [D][64]
-    constexpr int KV_PER_ROW = D / EPF;
-    for (int v = tid; v < BKEY * KV_PER_ROW; v += 256) {
+  // K [64][D] and V^T [D][64] of a key tile: loaded into registers during the
+  // previous tile's products, written to LDS after them
+  constexpr int KV_PER_ROW = D / EPF, V_PER_ROW = BKEY / EPF;
+  constexpr int NKL = BKEY * KV_PER_ROW / 256, NVL = D * V_PER_ROW / 256;  // vectors per thread
+  static_assert(BKEY * KV_PER_ROW % 256 == 0 && D * V_PER_ROW % 256 == 0, "whole passes");
+  vec kreg[NKL], vreg[NVL];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < NKL; ++u) {
+      const int v = tid + 256 * u;
       const int r = v / KV_PER_ROW, c = (v % KV_PER_ROW) * EPF;
       const int key = min(j0 + r, p.kn - 1);
-      *reinterpret_cast<vec*>(&sK[r * LDK + c]) = c < d ? *reinterpret_cast<const vec*>(K + (int64_t)key * d + c) : vec{};
+      kreg[u] = c < d ? *reinterpret_cast<const vec*>(K + (int64_t)key * d + c) : vec{};
     }
-    constexpr int V_PER_ROW = BKEY / EPF;
-    for (int v = tid; v < D * V_PER_ROW; v += 256) {
+#pragma unroll
+    for (int u = 0; u < NVL; ++u) {
+      const int v = tid + 256 * u;
       const int r = v / V_PER_ROW, c = (v % V_PER_ROW) * EPF;
       const int key = min(j0 + c, p.ldv - EPF);
-      vec vv = r < d ? *reinterpret_cast<const vec*>(V + (int64_t)r * p.ldv + key) : vec{};
+      vreg[u] = r < d ? *reinterpret_cast<const vec*>(V + (int64_t)r * p.ldv + key) : vec{};
+    }
+  };
+  auto store_tile = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < NKL; ++u) {
+      const int v = tid + 256 * u;
+      const int r = v / KV_PER_ROW, c = (v % KV_PER_ROW) * EPF;
+      *reinterpret_cast<vec*>(&sK[r * LDK + c]) = kreg[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NVL; ++u) {
+      const int v = tid + 256 * u;
+      const int r = v / V_PER_ROW, c = (v % V_PER_ROW) * EPF;
+      const int key = min(j0 + c, p.ldv - EPF);
+      vec vv = vreg[u];
 #pragma unroll
       for (int e = 0; e < EPF; ++e)
         if (key + e >= p.kn) vv[e] = T(0);  // keys past kn may be uninitialised
       *reinterpret_cast<vec*>(&sV[r * LDV + c]) = vv;
     }
-    lds_barrier();
+  };
+  load_tile(0);
+  store_tile(0);
+  lds_barrier();
+  for (int j0 = 0; j0 < key_end; j0 += BKEY) {
+    const bool more = j0 + BKEY < key_end;  // uniform over the work-group
+    if (more) load_tile(j0 + BKEY);
 
     // ---- S = Q K^T for 16 rows x 64 keys
     float4_t S[4];
@@ -120,9 +148,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
         S[nt][i] = s;
         mx = fmaxf(mx, s);
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      mt[i] = mx;
+      mt[i] = lane_max<16>(mx);
     }
     float rescale[4];
 #pragma unroll
@@ -137,8 +163,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
         S[nt][i] = pv;
         rs += pv;
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 64);
+      rs = lane_sum<16>(rs);  // the association of an xor butterfly
       l[i] = l[i] * rescale[i] + rs;
     }
 #pragma unroll
@@ -162,7 +187,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
 #pragma unroll
       for (int kb = 0; kb < BKEY / KB; ++kb) Mma<T>::mma(O[nt], pf[kb], load_frag<T>(bsrc + kb * KB));
     }
-    lds_barrier();  // sK / sV are restaged next iteration
+    lds_barrier();  // every wave is done with this tile's sK / sV
+    if (more) {
+      store_tile(j0 + BKEY);
+      lds_barrier();
+    }
   }
 
   // ---- epilogue: y = round(round(O / l) * round(sigmoid(gate)))

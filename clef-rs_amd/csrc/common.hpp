@@ -85,6 +85,16 @@ __device__ __forceinline__ float lane_sum(float v) {
   return v;
 }
 __device__ __forceinline__ float sum16(float v) { return lane_sum<16>(v); }
+// Maximum over groups of N = 2, 4, 8 or 16 consecutive lanes, by the same moves.
+template <int N>
+__device__ __forceinline__ float lane_max(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "2..16 lanes");
+  if constexpr (N >= 2) v = fmaxf(v, dpp_partner<0xB1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp_partner<0x4E>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp_partner<0x141>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp_partner<0x140>(v));
+  return v;
+}
 
 // Work-group barrier for LDS producer/consumer hand-offs only.  Unlike
 // __syncthreads() it does not wait for outstanding global loads, so register
