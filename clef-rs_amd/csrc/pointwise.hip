@@ -645,6 +645,42 @@ __global__ __launch_bounds__(256) void values_t_kernel(const void* x, int64_t ld
   }
 }
 
+// f16 in and out, d a multiple of 64, 16-byte aligned rows: a 64-token x
+// 64-feature tile moves as 16-byte vectors (8 features of a token in, 8
+// tokens of a feature out) through an LDS tile; the last group of a partial
+// tile is stored element by element.
+__global__ __launch_bounds__(256) void values_t_f16_kernel(const half_t* __restrict__ x, int64_t ldx,
+                                                           half_t* __restrict__ y, int64_t ldy_tok, int T, int d,
+                                                           int dst_offset) {
+  __shared__ __attribute__((aligned(16))) half_t tile[64][72];  // [token][feature], padded rows
+  const int h = blockIdx.z, t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const int r = i >> 3, c = (i & 7) * 8;
+    const int t = min(t0 + r, T - 1);
+    *reinterpret_cast<half8*>(&tile[r][c]) = *reinterpret_cast<const half8*>(x + (int64_t)t * ldx + (int64_t)h * d + e0 + c);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const int e = i >> 3, t8 = (i & 7) * 8;
+    if (t0 + t8 >= T) continue;
+    half8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = tile[t8 + j][e];
+    half_t* dst = y + ((int64_t)h * d + e0 + e) * ldy_tok + dst_offset + t0 + t8;
+    if (t0 + t8 + 8 <= T) {
+      *reinterpret_cast<half8*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (t0 + t8 + j < T) dst[j] = v[j];
+    }
+  }
+}
+
 // ---- embedding gather and pooled head ---------------------------------------
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, int T, const void* table, int dt,
                                                     int vocab, int H, float* h) {
@@ -983,8 +1019,15 @@ extern "C" int clef_values_transposed(const void* x, int64_t ldx, int dtype_in, 
   CLEF_REQUIRE(T >= 1 && heads >= 1 && d >= 1 && ldx >= (int64_t)heads * d, "values: dimensions");
   CLEF_REQUIRE(dst_offset >= 0 && ldy_tok >= (int64_t)dst_offset + T, "values: destination");
   CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "values: dtype");
-  hipLaunchKernelGGL(values_t_kernel, dim3((T + 63) / 64, (d + 63) / 64, heads), dim3(256), 0,
-                     (hipStream_t)stream, x, ldx, dtype_in, y, ldy_tok, dtype_out, T, heads, d, dst_offset);
+  const bool vec = dtype_in == CLEF_F16 && dtype_out == CLEF_F16 && d % 64 == 0 && ldx % 8 == 0 &&
+                   ldy_tok % 8 == 0 && dst_offset % 8 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(values_t_f16_kernel, dim3((T + 63) / 64, d / 64, heads), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const half_t*>(x), ldx, static_cast<half_t*>(y), ldy_tok, T, d, dst_offset);
+  else
+    hipLaunchKernelGGL(values_t_kernel, dim3((T + 63) / 64, (d + 63) / 64, heads), dim3(256), 0,
+                       (hipStream_t)stream, x, ldx, dtype_in, y, ldy_tok, dtype_out, T, heads, d, dst_offset);
   return check_launch("values_transposed");
 }
 

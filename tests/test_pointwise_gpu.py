@@ -96,6 +96,24 @@ def test_gated_rms_silu(clef, dt, T, Hv, width):
 
 
 @gpu
+@pytest.mark.parametrize("T,heads,d,offset", [(4096, 2, 256, 0), (1, 1, 64, 0), (65, 2, 128, 8), (4109, 2, 256, 512),
+                                               (77, 3, 64, 5), (300, 2, 24, 0)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_values_transposed_is_an_exact_transpose(clef, T, heads, d, offset, dt):
+    """clef_values_transposed: y[h, e, offset + t] = x[t, h*d + e] exactly, the
+    columns outside [offset, offset + T) untouched (the 16-byte f16 path for
+    d % 64 == 0 and 8-aligned offsets, partial last tiles, and the element path)."""
+    gen = torch.Generator(device="cuda").manual_seed(T + d)
+    x = torch.randn((T, heads * d), generator=gen, device="cuda").to(dt)
+    ld = ((offset + T + 63) // 64) * 64
+    out = torch.full((heads, d, ld), 7.0, dtype=dt, device="cuda")
+    clef.values_transposed(x, heads, d, out=out, dst_offset=offset)
+    ref = torch.full((heads, d, ld), 7.0, dtype=dt, device="cuda")
+    ref[:, :, offset:offset + T] = x.view(T, heads, d).permute(1, 2, 0)
+    assert torch.equal(out, ref)
+
+
+@gpu
 @pytest.mark.parametrize("heads,kvh,qn,kn,d", [(16, 2, 300, 300, 256), (2, 1, 20, 20, 8), (4, 2, 17, 273, 64),
                                                (2, 1, 1, 256, 256), (8, 8, 130, 130, 128)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
