@@ -23,7 +23,7 @@ int gemm_launch(const GemmParams& p, int epilogue, hipStream_t stream);
 // f16 large-M path (gemm_f16.hip)
 bool gemm_f16_dma_ok(const GemmParams& p);
 int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t stream);
-int gemm_f16_tile_width(const GemmParams& p, int epilogue);  // 256, 192 or 128
+int gemm_f16_tile_shape(const GemmParams& p, int epilogue, int* bm);  // width 256, 192 or 128; rows 256 or 128
 
 // a/b projections fused with the DeltaNet gates (gemm_f16.hip); f16 operands,
 // Hv in {16, 32, 64}, K % 256 == 0, K <= 4096, rows 16-byte aligned (checked

@@ -3,8 +3,9 @@
 // gemm.hip (neural.metal:7-125 tile GEMM, projection.rs:82-95); selected for
 // M >= 256, K % 64 == 0 and 16-byte aligned rows.
 //
-// A work-group of 8 waves (4 x 2, two per SIMD) computes a 256 x BN tile,
-// each wave 64 x BN/2 with v_mfma_f32_32x32x16_f16 (at most 128 accumulator
+// A work-group of 8 waves (4 x 2, two per SIMD) computes a 256 x BN tile
+// (or 128 x BN when 256-row tiles would leave CUs idle), each wave
+// BM/4 x BN/2 with v_mfma_f32_32x32x16_f16 (at most 128 accumulator
 // registers per wave, which the register allocator keeps in place).  K
 // advances in 64-element stages through two LDS buffers (three for 128-wide
 // tiles) filled by global->LDS DMA (global_load_lds_dwordx4, 1 KiB per wave
@@ -21,7 +22,7 @@
 namespace clef {
 namespace {
 
-constexpr int kBM = 256, kBK = 64;
+constexpr int kBM = 256, kBK = 64;  // largest row tile, K stage
 
 // global_load_lds_dwordx4 written as inline asm: the compiler does not see an
 // LDS write it would have to order before every later LDS read (it would
@@ -44,18 +45,18 @@ __device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N)
 }
 
 
-template <int BN, int VM, int NS, int EPI>
+template <int BM, int BN, int VM, int NS, int EPI>
 __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
-  constexpr int kWaves = VM * 2;
-  constexpr int WM = kBM / VM, WN = BN / 2;
+  constexpr int kWaves = VM * 2;  // VM wave rows x 2 wave columns
+  constexpr int WM = BM / VM, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int NA = kBM * 8 / 64 / kWaves;  // A DMA instructions per wave per stage
+  constexpr int NA = BM * 8 / 64 / kWaves;  // A DMA instructions per wave per stage
   constexpr int NB = BN * 8 / 64 / kWaves;
   typedef half8 frag;
 
-  // NS stages of the A (256 x 64) and B (BN x 64) tiles; after the last
+  // NS stages of the A (BM x 64) and B (BN x 64) tiles; after the last
   // stage the same bytes stage the accumulators for the epilogue
-  constexpr int kStA = kBM * kBK, kStB = BN * kBK;
+  constexpr int kStA = BM * kBK, kStB = BN * kBK;
   __shared__ __attribute__((aligned(1024))) half_t smem[NS * (kStA + kStB)];
   auto sA = [&](int st) { return smem + st * kStA; };
   auto sB = [&](int st) { return smem + NS * kStA + st * kStB; };
@@ -67,7 +68,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- tile index with XCD-compact placement (as gemm.hip)
-  const int tiles_m = (p.M + kBM - 1) / kBM;
+  const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN);
   const int ntiles = tiles_m * tiles_n;
   int t = blockIdx.x;
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   const int gm = min(group, tiles_m - first_m);
   const int tm = first_m + (t % gsize) % gm;
   const int tn = (t % gsize) / gm;
-  const int m0 = tm * kBM;
+  const int m0 = tm * BM;
   const int n0 = tn * (EPI == 2 ? BN / 2 : BN);
 
   const half_t* X = static_cast<const half_t*>(p.x);
@@ -282,16 +283,16 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   }
 }
 
-template <int BN, int EPI>
+template <int BM, int BN, int EPI>
 int launch(const GemmParams& p, hipStream_t s) {
-  constexpr int VM = 4;
-  // three stages where they fit in LDS (128-wide tiles: 3 x 48 KiB): the
-  // DMA then runs two stages ahead (whole prefill 1.4% faster, interleaved
-  // A/B, all from the residual GEMMs)
+  // three stages where they fit in LDS (128-wide tiles: 3 x 48 KiB, or
+  // 3 x 32 KiB for 128 x 128): the DMA then runs two stages ahead (whole
+  // prefill 1.4% faster, interleaved A/B, all from the residual GEMMs)
   constexpr int NS = BN == 128 ? 3 : 2;
-  const int tiles_m = (p.M + kBM - 1) / kBM;
+  const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_f16_dma<BN, VM, NS, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
+  constexpr int VM = 4;  // 8 waves, two per SIMD (WM = BM / 4 rows each)
+  hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NS, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
   return check_launch("gemm");
 }
 
@@ -451,29 +452,47 @@ static int device_cus() {
   return cached[dev];
 }
 
-// Tile width: one 256 x BN tile per CU at a time (the LDS holds one), so a
-// launch takes ceil(tiles / CUs) rounds, each as long as a tile; a narrower
-// tile costs a little more per column (fewer products per fragment read and
-// per byte moved).  The width with the least rounds x width x that cost wins,
-// e.g. 256 for N = 12288, 192 for N = 9216 (768 tiles: 3 full rounds instead
-// of 2.25), 128 for N = 2048 (256 tiles: one round).  SwiGLU keeps 256 or 128
-// (its wave columns pair gate and up blocks).
-int gemm_f16_tile_width(const GemmParams& p, int epilogue) {
+// Tile shape: one tile per CU at a time (the LDS holds one), so a launch
+// takes ceil(tiles / CUs) rounds, each as long as a tile; a smaller tile
+// costs a little more per output (fewer products per fragment read and per
+// byte moved).  The shape with the least rounds x area x that cost wins,
+// e.g. 256 x 256 for N = 12288, 256 x 192 for N = 9216 (768 tiles: 3 full
+// rounds instead of 2.25), 256 x 128 for M = 4096, N = 2048 (256 tiles: one
+// round), 128 x 128 for M = N = 2048 (256 tiles instead of 128 of 256 x 128,
+// which leave half the CUs idle).  SwiGLU keeps widths 256 or 128 (its wave
+// columns pair gate and up blocks).  Returns the width; *bm the row tile.
+int gemm_f16_tile_shape(const GemmParams& p, int epilogue, int* bm) {
   const int n_eff = epilogue == 2 ? 2 * p.N : p.N;
-  const long tm = (p.M + kBM - 1) / kBM, cus = device_cus();
-  auto cost = [&](int bn, double per_col) {
-    const long tiles = tm * ((n_eff + bn - 1) / bn);
-    return (double)((tiles + cus - 1) / cus) * bn * per_col;
+  const long cus = device_cus();
+  auto cost = [&](int rows, int bn, double per_out) {
+    const long tiles = (long)((p.M + rows - 1) / rows) * ((n_eff + bn - 1) / bn);
+    return (double)((tiles + cus - 1) / cus) * rows * bn * per_out;
   };
-  const double c256 = cost(256, 1.0), c192 = epilogue == 2 ? 1e300 : cost(192, 1.1), c128 = cost(128, 1.2);
-  return c256 <= c192 && c256 <= c128 ? 256 : (c192 <= c128 ? 192 : 128);
+  struct Cand { int bm, bn; double c; };
+  const Cand cands[] = {{256, 256, cost(256, 256, 1.0)},
+                        {256, 192, epilogue == 2 ? 1e300 : cost(256, 192, 1.1)},
+                        {256, 128, cost(256, 128, 1.2)},
+                        {128, 128, cost(128, 128, 1.5)}};
+  Cand best = cands[0];
+  for (const Cand& c : cands)
+    if (c.c < best.c) best = c;
+  *bm = best.bm;
+  return best.bn;
 }
 
 int gemm_f16_dma_launch(const GemmParams& p, int epilogue, hipStream_t s) {
-  const int bn = gemm_f16_tile_width(p, epilogue);
-  if (epilogue == 0) return bn == 256 ? launch<256, 0>(p, s) : bn == 192 ? launch<192, 0>(p, s) : launch<128, 0>(p, s);
-  if (epilogue == 1) return bn == 256 ? launch<256, 1>(p, s) : bn == 192 ? launch<192, 1>(p, s) : launch<128, 1>(p, s);
-  return bn == 256 ? launch<256, 2>(p, s) : launch<128, 2>(p, s);
+  int bm = kBM;
+  const int bn = gemm_f16_tile_shape(p, epilogue, &bm);
+  if (bm == 128) {
+    if (epilogue == 0) return launch<128, 128, 0>(p, s);
+    if (epilogue == 1) return launch<128, 128, 1>(p, s);
+    return launch<128, 128, 2>(p, s);
+  }
+  if (epilogue == 0)
+    return bn == 256 ? launch<256, 256, 0>(p, s) : bn == 192 ? launch<256, 192, 0>(p, s) : launch<256, 128, 0>(p, s);
+  if (epilogue == 1)
+    return bn == 256 ? launch<256, 256, 1>(p, s) : bn == 192 ? launch<256, 192, 1>(p, s) : launch<256, 128, 1>(p, s);
+  return bn == 256 ? launch<256, 256, 2>(p, s) : launch<256, 128, 2>(p, s);
 }
 
 }  // namespace clef
