@@ -97,15 +97,19 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
 #pragma unroll
   for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
   const int lrow = lane >> 3;
-  auto issue = [&](half_t* sa, half_t* sb, int k0) {
+  // (part / nparts: the instructions q with q % nparts == part, so a stage's
+  // DMA can be spread over the k-blocks of the stage before it)
+  auto issue = [&](half_t* sa, half_t* sb, int k0, int part = 0, int nparts = 1) {
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
+      if (q % nparts != part) continue;
       const int j = wave * NA + q;
       const int row = min(m0 + 8 * j + lrow, p.M - 1);
       dma16(X + row * (int)p.ldx + lcol[j & 1] + k0, sa + j * 512);
     }
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
+      if (q % nparts != part) continue;
       const int j = wave * NB + q;
       const int row = 8 * j + lrow;
       const half_t* src;
@@ -135,8 +139,9 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   int foff[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) foff[kb] = 2 * (frow * kBK + (((2 * kb + fkc) ^ ((frow >> 1) & 7)) << 3));
-  // k-block kb+1's fragments are requested before kb's products
-  auto compute = [&](const half_t* sa, const half_t* sb) {
+  // k-block kb+1's fragments are requested during kb's products; dma(kb)
+  // issues part kb of a later stage's DMA before them
+  auto compute = [&](const half_t* sa, const half_t* sb, auto&& dma) {
     const char* ab = reinterpret_cast<const char*>(sa) + wm * WM * kBK * 2;
     const char* bb = reinterpret_cast<const char*>(sb) + wn * WN * kBK * 2;
     frag af[2][TM], bf[2][TN];
@@ -149,12 +154,25 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     load(0);
 #pragma unroll
     for (int kb = 0; kb < kBK / 16; ++kb) {
+      dma(kb);
       if (kb + 1 < kBK / 16) load(kb + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kb & 1][i], bf[kb & 1][j], acc[i][j], 0, 0, 0);
+      // one fragment read of k-block kb+1 after each product of kb, so the
+      // reads stream under the products and are in long before their use
+      // (the compiler otherwise issues them late and waits on them; 2-5%
+      // faster on the in-projection and SwiGLU shapes with the weights
+      // cache-resident, neutral in a whole prefill; bit-identical)
+      if (kb + 1 < kBK / 16) {
+#pragma unroll
+        for (int q = 0; q < TM + TN; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -175,8 +193,13 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   for (int kt = 0; kt < nk; ++kt) {
     const int nxt = cur + NS - 1 >= NS ? cur - 1 : cur + NS - 1;  // (cur + NS - 1) % NS
     const bool more = kt + NS - 1 < nk;
-    if (more) issue(sA(nxt), sB(nxt), (kt + NS - 1) * kBK);
-    compute(sA(cur), sB(cur));
+    // stage kt+NS-1's DMA, half before each of the first two k-blocks'
+    // products (whole prefill 0.7% faster than all of it at the stage start,
+    // by interleaved A/B; spread over all four k-blocks, the last quarter
+    // has too little time to land when the weights come from HBM: 2% slower)
+    compute(sA(cur), sB(cur), [&](int kb) {
+      if (more && kb < 2) issue(sA(nxt), sB(nxt), (kt + NS - 1) * kBK, kb, 2);
+    });
     if (NS == 3 && more)
       vm_wait<NA + NB>();
     else
