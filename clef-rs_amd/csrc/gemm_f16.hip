@@ -15,6 +15,7 @@
 // distinct bank groups.  The DMA lanes pick their source chunk so that the
 // lane-ordered LDS writes produce that layout.
 #include <algorithm>
+#include <utility>
 
 #include "common.hpp"
 #include "gemm.hpp"
@@ -43,9 +44,15 @@ __device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N)
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+// vmcnt(n) for an n that is a constant once loops are unrolled
+template <int... Ns>
+__device__ __forceinline__ void vm_wait_n(int n, std::integer_sequence<int, Ns...>) {
+  ((n == Ns ? (vm_wait<Ns>(), 0) : 0), ...);
+}
+__device__ __forceinline__ void vm_wait_n(int n) { vm_wait_n(n, std::make_integer_sequence<int, 40>{}); }
 
 
-template <int BM, int BN, int VM, int NS, int EPI>
+template <int BM, int BN, int VM, int NSA, int NSB, int EPI>
 __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int kWaves = VM * 2;  // VM wave rows x 2 wave columns
   constexpr int WM = BM / VM, WN = BN / 2;
@@ -54,13 +61,13 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int NB = BN * 8 / 64 / kWaves;
   typedef half8 frag;
 
-  // NS stages of the A (BM x 64) and B (BN x 64) tiles; after the last
+  // rings of NSA A (BM x 64) and NSB B (BN x 64) stages; after the last
   // stage the same bytes stage the accumulators for the epilogue
   constexpr int kStA = BM * kBK, kStB = BN * kBK;
-  __shared__ __attribute__((aligned(1024))) half_t smem[NS * (kStA + kStB)];
+  __shared__ __attribute__((aligned(1024))) half_t smem[NSA * kStA + NSB * kStB];
   auto sA = [&](int st) { return smem + st * kStA; };
-  auto sB = [&](int st) { return smem + NS * kStA + st * kStB; };
-  static_assert(NS == 2 || NS == 3, "two or three LDS stages");
+  auto sB = [&](int st) { return smem + NSA * kStA + st * kStB; };
+  static_assert((NSA == 2 || NSA == 3) && (NSB == NSA || NSB == NSA + 1), "two or three stages per operand");
   static_assert(kWaves * 32 * WN * 4 <= (int)sizeof(smem), "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -98,18 +105,19 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
   const int lrow = lane >> 3;
   // (part / nparts: the instructions q with q % nparts == part, so a stage's
-  // DMA can be spread over the k-blocks of the stage before it)
+  // DMA can be spread over the k-blocks of the stage before it; a null sa or
+  // sb skips that operand)
   auto issue = [&](half_t* sa, half_t* sb, int k0, int part = 0, int nparts = 1) {
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
-      if (q % nparts != part) continue;
+      if (q % nparts != part || !sa) continue;
       const int j = wave * NA + q;
       const int row = min(m0 + 8 * j + lrow, p.M - 1);
       dma16(X + row * (int)p.ldx + lcol[j & 1] + k0, sa + j * 512);
     }
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
-      if (q % nparts != part) continue;
+      if (q % nparts != part || !sb) continue;
       const int j = wave * NB + q;
       const int row = 8 * j + lrow;
       const half_t* src;
@@ -177,35 +185,100 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     }
   };
 
-  // NS-stage ring: stage kt+NS-1 is requested while stage kt is multiplied;
-  // each wave then waits for its own requests of stage kt+1 (the newest
-  // NS-2 stages may stay in flight) before the barrier that publishes it.
+  // Rings: stage kt+NSA-1 of A and kt+NSB-1 of B are requested while stage
+  // kt is multiplied; each wave then waits for its own requests of stage
+  // kt+1 before the barrier that publishes it.  Requests complete in issue
+  // order, so what may stay in flight at that wait is what was issued after
+  // stage kt+1's last request: stage kt+2 of each three-slot operand (with
+  // NSA = 2, NSB = 3 the A stage kt+1 is issued before the B stage kt+2).
+  constexpr int KEEP = (NSA == 3 ? NA : 0) + (NSB == 3 ? NB : 0);
   const int nk = p.K / kBK;
-#pragma unroll
-  for (int st = 0; st < NS - 1; ++st)
-    if (st < nk) issue(sA(st), sB(st), st * kBK);
-  if (NS == 3 && nk > 1)
-    vm_wait<NA + NB>();
-  else
+  auto wait_next = [&](int kt) {  // before the barrier that publishes stage kt+1
+    if constexpr (KEEP > 0) {
+      if (kt + 2 < nk) {
+        vm_wait<KEEP>();
+        return;
+      }
+    }
     vm_wait_all();
+  };
+#pragma unroll
+  for (int st = 0; st < NSB - 1; ++st) {
+    if (st < NSA - 1 && st < nk) issue(sA(st), nullptr, st * kBK);
+    if (st < nk) issue(nullptr, sB(st), st * kBK);
+  }
+  wait_next(-1);
   lds_barrier();
-  int cur = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int nxt = cur + NS - 1 >= NS ? cur - 1 : cur + NS - 1;  // (cur + NS - 1) % NS
-    const bool more = kt + NS - 1 < nk;
-    // stage kt+NS-1's DMA, half before each of the first two k-blocks'
-    // products (whole prefill 0.7% faster than all of it at the stage start,
-    // by interleaved A/B; spread over all four k-blocks, the last quarter
-    // has too little time to land when the weights come from HBM: 2% slower)
-    compute(sA(cur), sB(cur), [&](int kb) {
-      if (more && kb < 2) issue(sA(nxt), sB(nxt), (kt + NS - 1) * kBK, kb, 2);
+
+  // Residual tiles (EPI 1, 128-wide) are read into registers over the last
+  // kPD stages, NRB float4 per lane per stage, instead of in the epilogue:
+  // every tile of a one-round launch ends at about the same time, and their
+  // residual reads would otherwise meet in one burst after the products.
+  // Row r, column c of slab i, chunk q are the epilogue's (below).
+  constexpr int OW = EPI == 2 ? WN / 2 : WN;  // output columns per wave
+  constexpr int CPR = OW / 4;                  // 4-column chunks per row
+  constexpr int PER = 32 * CPR / 64;           // chunks per lane per slab
+  constexpr bool PF = EPI == 1 && BN == 128;
+  constexpr int kPD = 8, NR = TM * PER, NRB = NR / kPD;
+  static_assert(!PF || NR % kPD == 0, "prefetch batches");
+  const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
+  const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
+  const bool pf = PF && yvec && nk >= kPD && m0 + BM <= p.M && n0 + BN <= p.N;
+  float4 pre[PF ? NR : 1];
+  auto prefetch = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < NRB; ++u) {
+      const int e = b * NRB + u, i = e / PER, q = e % PER, idx = q * 64 + lane;
+      const int r = m0 + wm * WM + i * 32 + idx / CPR, c = n0 + wn * OW + (idx % CPR) * 4;
+      pre[e] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.y) + (int64_t)r * p.ldy + c);
+    }
+  };
+
+  int ca = 0, cb = 0;
+  auto stage = [&](int kt) {
+    const int na = ca == 0 ? NSA - 1 : ca - 1;  // (ca + NSA - 1) % NSA
+    const int nb = cb == 0 ? NSB - 1 : cb - 1;
+    const bool more_a = kt + NSA - 1 < nk, more_b = kt + NSB - 1 < nk;
+    compute(sA(ca), sB(cb), [&](int kb) {
+      if constexpr (NSA == NSB) {
+        // the next stage's DMA, half before each of the first two k-blocks'
+        // products (whole prefill 0.7% faster than all of it at the stage
+        // start, by interleaved A/B; spread over all four k-blocks, the last
+        // quarter has too little time to land when the weights come from HBM:
+        // 2% slower)
+        if (more_a && kb < 2) issue(sA(na), sB(nb), (kt + NSA - 1) * kBK, kb, 2);
+      } else {
+        // A one stage ahead before k-block 0, B two stages ahead before
+        // k-block 1 (in that order: see wait_next)
+        if (more_a && kb == 0) issue(sA(na), nullptr, (kt + NSA - 1) * kBK);
+        if (more_b && kb == 1) issue(nullptr, sB(nb), (kt + NSB - 1) * kBK);
+      }
     });
-    if (NS == 3 && more)
-      vm_wait<NA + NB>();
-    else
-      vm_wait_all();
+  };
+  auto advance = [&]() {
+    ca = ca + 1 == NSA ? 0 : ca + 1;
+    cb = cb + 1 == NSB ? 0 : cb + 1;
+  };
+  const int kmain = pf ? nk - kPD : nk;
+  for (int kt = 0; kt < kmain; ++kt) {
+    stage(kt);
+    wait_next(kt);
     lds_barrier();
-    cur = cur + 1 == NS ? 0 : cur + 1;
+    advance();
+  }
+  if constexpr (PF) {
+    if (pf) {
+#pragma unroll
+      for (int d = 0; d < kPD; ++d) {
+        stage(nk - kPD + d);
+        prefetch(d);
+        // issued after stage kt+1's last request: batch d-1, stage kt+2's
+        // DMA (NSA = NSB = 3 here) and batch d
+        vm_wait_n((d >= 1 ? NRB : 0) + (d + 2 < kPD ? NA + NB : 0) + NRB);
+        lds_barrier();
+        advance();
+      }
+    }
   }
 
   // ---- epilogue.  The loop's last barrier follows every wave's last
@@ -217,11 +290,6 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   // write -> read -> next write sequence needs no barrier.)
   float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
   const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
-  constexpr int OW = EPI == 2 ? WN / 2 : WN;  // output columns per wave
-  constexpr int CPR = OW / 4;                  // 4-column chunks per row
-  constexpr int PER = 32 * CPR / 64;           // chunks per lane per slab
-  const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
-  const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -252,9 +320,14 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       }
     }
     if (EPI == 1) {
-      // residual reads all issued before the first store
+      // residual reads all issued before the first store (or made during
+      // the last stages)
 #pragma unroll
       for (int q = 0; q < PER; ++q) {
+        if (PF && pf) {
+          res[q] = pre[PF ? i * PER + q : 0];
+          continue;
+        }
         const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
         const float* src = static_cast<const float*>(p.y) + (int64_t)r * p.ldy + c;
         if (yvec && r < p.M && c + 3 < p.N) {
@@ -310,12 +383,14 @@ template <int BM, int BN, int EPI>
 int launch(const GemmParams& p, hipStream_t s) {
   // three stages where they fit in LDS (128-wide tiles: 3 x 48 KiB, or
   // 3 x 32 KiB for 128 x 128): the DMA then runs two stages ahead (whole
-  // prefill 1.4% faster, interleaved A/B, all from the residual GEMMs)
-  constexpr int NS = BN == 128 ? 3 : 2;
+  // prefill 1.4% faster, interleaved A/B, all from the residual GEMMs).
+  // Wider tiles keep two A stages and three B (weight) stages: 160 KiB at
+  // 256 x 256, 136 KiB at 256 x 192.
+  constexpr int NSA = BN == 128 ? 3 : 2, NSB = 3;
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   constexpr int VM = 4;  // 8 waves, two per SIMD (WM = BM / 4 rows each)
-  hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NS, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
+  hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
   return check_launch("gemm");
 }
 
