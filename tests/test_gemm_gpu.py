@@ -64,7 +64,12 @@ def test_gemm_projection_shapes(clef, N, dtype):
 
 @gpu
 @pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8), (300, 203, 128),
-                                   (4096, 3000, 256)])
+                                   (4096, 3000, 256),
+                                   # residual tiles read during the last eight K stages: full and
+                                   # partial tiles in one launch, exactly eight stages, an odd row
+                                   # pitch (no vector access), 128 x 128 tiles
+                                   (1000, 2000, 1024), (768, 2048, 512), (600, 2001, 1024),
+                                   (256, 1024, 768)])
 def test_gemm_residual_epilogue(clef, M, N, K):
     x, w = _inputs(3, M, N, K, torch.float16)
     h = torch.randn((M, N), device="cuda")
@@ -78,10 +83,10 @@ def test_gemm_residual_epilogue(clef, M, N, K):
 
 
 @gpu
-@pytest.mark.parametrize("M,N,K", [(512, 256, 256), (300, 203, 128)])
+@pytest.mark.parametrize("M,N,K", [(512, 256, 256), (300, 203, 128), (1024, 1024, 1024)])
 def test_gemm_residual_epilogue_unrounded(clef, M, N, K):
     """Residual add of the f32 accumulator itself (no half rounding), aligned
-    and ragged rows."""
+    and ragged rows, and residual tiles read during the last K stages."""
     x, w = _inputs(8, M, N, K, torch.float16)
     h = torch.randn((M, N), device="cuda")
     h0 = h.clone()
