@@ -7,9 +7,10 @@
 // (or 128 x BN when 256-row tiles would leave CUs idle), each wave
 // BM/4 x BN/2 with v_mfma_f32_32x32x16_f16 (at most 128 accumulator
 // registers per wave, which the register allocator keeps in place).  K
-// advances in 64-element stages through two LDS buffers (three for 128-wide
-// tiles) filled by global->LDS DMA (global_load_lds_dwordx4, 1 KiB per wave
-// instruction): while a stage is multiplied the next one or two land.
+// advances in 64-element stages through LDS rings filled by global->LDS DMA
+// (global_load_lds_dwordx4, 1 KiB per wave instruction): three slots per
+// operand for 128-wide tiles, two activation and three weight slots for
+// wider ones, so a stage's weights land two stages ahead of their use.
 // Rows are 128 bytes; the 16-byte chunk c of row r is stored at slot
 // c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit 16
 // distinct bank groups.  The DMA lanes pick their source chunk so that the
