@@ -424,6 +424,326 @@ __global__ __launch_bounds__(256) void attn_f16(AttnParams p) {
   }  // work items (the last key tile ended with a barrier: LDS is free)
 }
 
+// ---------------------------------------------------------------------------
+// Single-sequence core at two waves per SIMD: a work-group of 8 waves owns
+// 128 queries of one head, wave w queries q0 + 16 w + (0..15), on
+// v_mfma_f32_16x16x32_f16 (A and B fragments: 8 consecutive k of row or
+// column lane % 16; accumulators: rows 4 (lane / 16) + i of column lane % 16).
+// S^T = K Q^T gives lane l its query l % 16 and, per 16-key tile t, 4 keys;
+// the query's 64 keys of a tile sit in the four lane groups l / 16, which
+// combine for the row maximum (the row sum is combined once, at the end).
+// Within each 32-key block the LDS key row [u g j] (u: bit 4, g: bits 2-3,
+// j: bits 0-1) holds key [g u j], so that the accumulators a lane holds of
+// tiles 2b, 2b+1 are its B-operand fragment (8 consecutive keys) of
+// O^T = V^T P^T for key block b.  About 200 registers: two waves per SIMD.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int key_perm16(int r) {
+  return (r & ~31) | (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
+  constexpr int BQ = 128, BK = 64, NW = 8;
+  constexpr int KS = D / 8;           // 16-byte chunks per key row
+  constexpr int NKS = D / 32;         // 32-deep k-steps of S^T = K Q^T
+  constexpr int NDT = D / 16;         // 16-row tiles of O^T
+  constexpr int KROWS = 512 / D;      // key rows per 1 KiB DMA instruction
+  constexpr int NDK = BK / KROWS / NW;  // K DMA instructions per wave and tile
+  constexpr int NDV = D / 8 / NW;       // V^T DMA instructions (8 rows of 64 keys each)
+  constexpr int PD = 4;               // LDS fragment reads in flight ahead of the MFMAs
+  static_assert(D == 256 || D == 128, "head width");
+  static_assert(NDK >= 1 && NDV >= 1, "whole DMA instructions per wave");
+
+  __shared__ __attribute__((aligned(1024))) half_t sK[2][BK * D];
+  __shared__ __attribute__((aligned(1024))) half_t sV[2][D * BK];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+
+  // work items dealt as in attn_f16 (longest first, boustrophedon)
+  const int nitems = ((p.qn + BQ - 1) / BQ) * p.heads;
+  const int nwg = gridDim.x;
+  for (int round = 0;; ++round) {
+  const int item = round * nwg + ((round & 1) ? nwg - 1 - (int)blockIdx.x : (int)blockIdx.x);
+  if (item >= nitems) break;
+  const int rank = item / p.heads, hi = item % p.heads;
+  const int h = (p.heads & 7) == 0 ? (hi & 7) * (p.heads >> 3) + (hi >> 3) : hi;
+  const int qn = p.qn, kn = p.kn;
+  const int q0 = ((qn + BQ - 1) / BQ - 1 - rank) * BQ;
+  const int kvh = h / (p.heads / p.kvh);
+  const int offset = kn - qn;
+  const int d = p.d;
+
+  const half_t* Q = static_cast<const half_t*>(p.q) + (int64_t)h * p.ldq * d;
+  const half_t* Kb = static_cast<const half_t*>(p.k) + (int64_t)kvh * p.ldk * d;
+  const half_t* Vb = static_cast<const half_t*>(p.vt) + (int64_t)kvh * d * p.ldv;
+
+  // Q^T fragments (B operand): lane (n, g) holds d = 32 s + 8 g .. + 7 of its query
+  half8 qf[NKS];
+  {
+    const int r = min(q0 + 16 * wave + n, qn - 1);
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int c = 32 * s + 8 * g;
+      qf[s] = c < d ? *reinterpret_cast<const half8*>(Q + (int64_t)r * d + c) : half8{};
+    }
+  }
+
+  // ---- DMA sources.  K instruction t = wave * NDK + q writes 1 KiB: rows
+  // t * KROWS + lane / KS, slot lane % KS holding chunk slot ^ (row & 15) of
+  // key key_perm16(row).  V^T instruction t: d-row 8 t + lane / 8, slot
+  // lane % 8 holding keys 8 c .. 8 c + 7 with c = slot ^ ((row >> 1) & 7).
+  // d past the head width reads in-bounds data that multiplies zero queries
+  // (K) or lands in unstored outputs (V); the last tile clamps keys to kn - 1
+  // (K, masked) and ldv - 8 (V, zeroed below).
+  uint32_t ko[NDK], vo[NDV];
+  int kr[NDK];
+#pragma unroll
+  for (int q = 0; q < NDK; ++q) {
+    const int row = (wave * NDK + q) * KROWS + lane / KS;
+    kr[q] = key_perm16(row);
+    const int kc = 8 * min((lane % KS) ^ (row & 15), d / 8 - 1);
+    ko[q] = 2u * (uint32_t)(kr[q] * d + kc);
+  }
+#pragma unroll
+  for (int q = 0; q < NDV; ++q) {
+    const int vrow = (wave * NDV + q) * 8 + (lane >> 3);
+    const int vc = 8 * ((lane & 7) ^ ((vrow >> 1) & 7));
+    vo[q] = 2u * (uint32_t)(min(vrow, d - 1) * (int)p.ldv + vc);
+  }
+  const int kn1 = kn - 1, ldv8 = (int)p.ldv - 8;
+  auto issue_k = [&](int buf, int j0) {
+    if (j0 + BK <= kn) {
+#pragma unroll
+      for (int q = 0; q < NDK; ++q) dma16s(Kb + (int64_t)j0 * d, ko[q], &sK[buf][(wave * NDK + q) * 512]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NDK; ++q) {
+        const int key = min(j0 + kr[q], kn1);
+        const char* src = reinterpret_cast<const char*>(Kb + (int64_t)key * d) + (ko[q] - 2u * (uint32_t)(kr[q] * d));
+        dma16(src, &sK[buf][(wave * NDK + q) * 512]);
+      }
+    }
+  };
+  auto issue_v = [&](int buf, int j0) {
+    if (j0 + BK <= kn) {
+#pragma unroll
+      for (int q = 0; q < NDV; ++q) dma16s(Vb + j0, vo[q], &sV[buf][(wave * NDV + q) * 512]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NDV; ++q) {
+        const int vrow = min((wave * NDV + q) * 8 + (lane >> 3), d - 1);
+        const int c0 = j0 + 8 * ((lane & 7) ^ ((((wave * NDV + q) * 8 + (lane >> 3)) >> 1) & 7));
+        dma16(Vb + ((int64_t)vrow * p.ldv + min(c0, ldv8)), &sV[buf][(wave * NDV + q) * 512]);
+      }
+    }
+  };
+
+  // ---- fragment read offsets (bytes).  K: row 16 t + n, chunk 4 s + g at
+  // slot chunk ^ n (row & 15 = n); V^T: row 16 u + n, chunk 4 kb + g at slot
+  // chunk ^ ((n >> 1) & 7).  The rest of each address is an immediate.
+  constexpr int KPER = 4;  // k-steps per 16-chunk swizzle period (the XOR keeps chunk bit 4)
+  int koff[KPER], voff[2];
+#pragma unroll
+  for (int x = 0; x < KPER; ++x) koff[x] = n * 2 * D + 16 * ((4 * x + g) ^ n);
+#pragma unroll
+  for (int x = 0; x < 2; ++x) voff[x] = n * 128 + 16 * ((4 * x + g) ^ ((n >> 1) & 7));
+  // S step i: key tile i % 4, k-step i / 4; PV step i: d tile i % NDT, key block i / NDT
+  auto kread = [&](const char* base, int i) {
+    const int t = i & 3, s = i >> 2;
+    return *reinterpret_cast<const half8*>(base + koff[s % KPER] + (s / KPER) * 16 * 16 + t * 16 * 2 * D);
+  };
+  auto vread = [&](const char* base, int i) {
+    return *reinterpret_cast<const half8*>(base + voff[i / NDT] + (i % NDT) * 16 * 128);
+  };
+  constexpr int NS1 = 4 * NKS, NS2 = 2 * NDT;
+  auto frag = [&](const char* kbase, const char* vbase, int st) {
+    return st < NS1 ? kread(kbase, st) : vread(vbase, st - NS1);
+  };
+
+  float4_t O[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) O[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float l_run = 0.0f;
+
+  const float c2 = p.scale * 1.4426950408889634f;  // scores to log2 units
+  const int key_end = min(kn, offset + q0 + BQ);
+  const int ntiles = (key_end + BK - 1) / BK;
+  const int lim = min(offset + q0 + 16 * wave + n, kn1);
+  // key offset within a tile of accumulator element (t, i): LDS row
+  // 16 t + 4 g + i holds key 32 (t / 2) + 8 g + 4 (t % 2) + i
+  auto kof = [&](int t, int i) { return 32 * (t >> 1) + 4 * (t & 1) + i + 8 * g; };
+  auto row_max = [](float x) {
+    x = fmaxf(x, __shfl_xor(x, 16, 64));
+    return fmaxf(x, __shfl_xor(x, 32, 64));
+  };
+
+  // ---- prologue: K(0), K(1), V(0) resident; scores of tile 0
+  issue_k(0, 0);
+  if (ntiles > 1) issue_k(1, BK);
+  issue_v(0, 0);
+  vm_wait_all();
+  lds_barrier();
+  float4_t Sc[4], Sn[4];
+  half8 fb[PD];
+  {
+    const char* kbase = reinterpret_cast<const char*>(sK[0]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) Sc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < PD; ++i) fb[i] = kread(kbase, i);
+#pragma unroll
+    for (int i = 0; i < NS1; ++i) {
+      Sc[i & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[i % PD], qf[i >> 2], Sc[i & 3], 0, 0, 0);
+      if (i + PD < NS1) fb[i % PD] = kread(kbase, i + PD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float m_ref;
+  {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sv = kof(t, i) > lim ? -INFINITY : Sc[t][i];
+        Sc[t][i] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    m_ref = row_max(mx);  // finite: every query sees key 0
+  }
+  lds_barrier();  // all waves are done with K(0) before K(2) replaces it
+
+  // ---- software pipeline over key tiles (as attn_f16): iteration j, with
+  // K(j+1) and V(j) resident and the masked scores of tile j in Sc:
+  //   phase 1: MFMA  Sn = K(j+1) Q^T        VALU  P = exp2(Sc c - m c), row sum
+  //   phase 2: MFMA  O^T += V(j)^T P^T      VALU  mask Sn, row max of tile j+1
+  for (int j = 0; j < ntiles; ++j) {
+    const int j0 = j * BK;
+    if (j + 2 < ntiles) issue_k(j & 1, j0 + 2 * BK);
+    if (j + 1 < ntiles) issue_v((j + 1) & 1, j0 + BK);
+    if (j0 + BK > kn) {  // last tile runs past the keys: zero those value columns
+      half_t* v = sV[j & 1];
+      for (int x = tid; x < D * 8; x += 512) {
+        const int r = x >> 3, slot = x & 7;
+        const int k0 = j0 + 8 * (slot ^ ((r >> 1) & 7));
+        if (k0 + 8 > kn) {
+          half8 val = *reinterpret_cast<half8*>(v + r * 64 + slot * 8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k0 + e >= kn) val[e] = half_t(0);
+          *reinterpret_cast<half8*>(v + r * 64 + slot * 8) = val;
+        }
+      }
+      lds_barrier();
+    }
+    const char* kbase = reinterpret_cast<const char*>(sK[(j + 1) & 1]);
+    const char* vbase = reinterpret_cast<const char*>(sV[j & 1]);
+    const float mc = m_ref * c2;
+    const int thr = lim - (j0 + BK);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) Sn[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    half8 pf[2];
+    float ps = 0.0f, mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PD; ++i) fb[i] = frag(kbase, vbase, i);
+    // phase 1: one probability every second score MFMA (16 per lane and tile)
+#pragma unroll
+    for (int st = 0; st < NS1; ++st) {
+      Sn[st & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[st % PD], qf[st >> 2], Sn[st & 3], 0, 0, 0);
+      fb[st % PD] = frag(kbase, vbase, st + PD);
+      if ((st & 1) == 0) {
+        const int x = st >> 1, t = x >> 2, i = x & 3;  // element (t, i): key block t / 2, slot 4 (t % 2) + i
+        const float pv = __builtin_amdgcn_exp2f(fmaf(Sc[t][i], c2, -mc));
+        ps += pv;
+        pf[t >> 1][4 * (t & 1) + i] = static_cast<half_t>(pv);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // phase 2: one masked score of tile j+1 every second PV MFMA, two MFMAs
+    // behind the end of the score chain
+    auto mask_max = [&](int x) {
+      const int t = x >> 2, i = x & 3;
+      const float sv = kof(t, i) > thr ? -INFINITY : Sn[t][i];
+      Sc[t][i] = sv;  // phase 1 is done with tile j's scores
+      mx = fmaxf(mx, sv);
+    };
+#pragma unroll
+    for (int i = 0; i < NS2; ++i) {
+      O[i % NDT] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[(NS1 + i) % PD], pf[i / NDT], O[i % NDT], 0, 0, 0);
+      if (NS1 + i + PD < NS1 + NS2) fb[(NS1 + i) % PD] = frag(kbase, vbase, NS1 + i + PD);
+      if (i >= 2 && ((i - 2) & 1) == 0 && (i - 2) / 2 < 16) mask_max((i - 2) / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int x = (NS2 - 2) / 2; x < 16; ++x) mask_max(x);
+    l_run += ps;
+    if (j + 1 < ntiles) {
+      // lazy rescale: move the reference only when exp2 would exceed 2^8
+      const float m_new = fmaxf(m_ref, row_max(mx));
+      if (__builtin_amdgcn_ballot_w64((m_new - m_ref) * c2 > 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f((m_ref - m_new) * c2);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) O[t] = O[t] * alpha;
+        l_run *= alpha;
+        m_ref = m_new;
+      }
+    }
+    vm_wait_all();
+    lds_barrier();
+  }
+
+  // ---- epilogue: y = round(round(O / l) * round(sigmoid(gate))); O^T
+  // accumulator t holds d = 16 t + 4 g + i of the lane's query
+  float lt = l_run + __shfl_xor(l_run, 16, 64);
+  lt += __shfl_xor(lt, 32, 64);
+  const float inv = 1.0f / lt;
+  const int row = q0 + 16 * wave + n;
+  const int64_t prow = min(row, qn - 1);
+  const half_t* gate = static_cast<const half_t*>(p.gate) + prow * p.ldg + (int64_t)h * p.hsg;
+  half_t* y = static_cast<half_t*>(p.y) + prow * p.ldy + (int64_t)h * d;
+  auto out4 = [&](int t, half4 gv) {
+    half4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = static_cast<float>(to_f16(O[t][e] * inv));
+      const float sg = static_cast<float>(to_f16(sigmoid_hw(static_cast<float>(gv[e]))));
+      r[e] = static_cast<half_t>(a * sg);
+    }
+    return r;
+  };
+  if (p.vec_io) {
+    half4 gv[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const int d0 = 16 * t + 4 * g;
+      gv[t] = d0 < d ? *reinterpret_cast<const half4*>(gate + d0) : half4{};
+    }
+    if (row < qn) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const int d0 = 16 * t + 4 * g;
+        if (d0 < d) *reinterpret_cast<half4*>(y + d0) = out4(t, gv[t]);
+      }
+    }
+  } else if (row < qn) {
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const int d0 = 16 * t + 4 * g;
+      if (d0 < d) {
+        half4 gv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gv[e] = gate[d0 + e];
+        const half4 r = out4(t, gv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[d0 + e] = r[e];
+      }
+    }
+  }
+  }  // work items (the last key tile ended with a barrier: LDS is free)
+}
+
 // Query tiles of a ragged batch (one work-group, ragged.hpp): the monotone
 // spans (written to `spans`, which the attention kernel then reads as its
 // sequence offsets), and per sequence its tiles of 128 queries ranked by key
@@ -484,6 +804,28 @@ int launch(const AttnParams& p0, hipStream_t s) {
   return check_launch("attention");
 }
 
+// the single-sequence core at two waves per SIMD
+constexpr bool kW8 = true;
+template <int D>
+int launch_w8(const AttnParams& p0, hipStream_t s) {
+  AttnParams p = p0;
+  p.vec_io = ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.y)) & 7) == 0 &&
+             p.ldg % 4 == 0 && p.hsg % 4 == 0 && p.ldy % 4 == 0 && p.d % 4 == 0;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16_w8<D>, 512, 0) != hipSuccess || per <= 0) per = 1;
+    cached[dev] = cus * per;
+  }
+  const int items = (p.qn + 127) / 128 * p.heads;
+  const int groups = items < cached[dev] ? items : cached[dev];
+  hipLaunchKernelGGL((attn_f16_w8<D>), dim3(groups), dim3(512), 0, s, p);
+  return check_launch("attention");
+}
+
 }  // namespace
 
 // Workspace: pairs [tiles] int2, keys [tiles] int, the pair count, spans
@@ -524,6 +866,7 @@ bool attn_f16_ok(const AttnParams& p) {
 }
 
 int attn_f16_launch(const AttnParams& p, hipStream_t s) {
+  if (kW8 && !p.cu_q && p.d > 128) return launch_w8<256>(p, s);
   if (p.d <= 64) return launch<64>(p, s);
   if (p.d <= 128) return launch<128>(p, s);
   return launch<256>(p, s);
