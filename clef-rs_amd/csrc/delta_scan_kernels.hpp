@@ -584,14 +584,20 @@ struct Carry {
   static constexpr int SPR = G::NST / NREC;               // its 16-row tiles
   static constexpr int XCH = NREC > 1 ? NREC * 4096 : 0;  // partial products Y_r
   // waves: NREC recurrence, NLOAD loaders, NOUT output waves of TPW 16-row tiles
-  // (one f32 recurrence wave leaves room for two output waves of 512 registers)
+  // (one f32 recurrence wave leaves room for two output waves of 512 registers).
+  // (f16 with three loaders, eight waves, takes the same time: the chunk's
+  // DMA costs the products it shares the CU with, not its own issue rate or
+  // latency; f32 already has nine waves.)
   static constexpr int NLOAD = sizeof(CT) == 2 ? 2 : 1;
   static constexpr int NOUT = (sizeof(CT) == 4 && NREC == 1) ? 2 : 4;
   static constexpr int TPW = 4 / NOUT;
   static constexpr int OD = (sizeof(CT) == 4 && NOUT == 4) ? 1 : 2;  // chunks of output operands in registers
+  // a chunk's DMA items: NDK key blocks, NBU U blocks, one block of row
+  // scalars; loader w issues items [w PERW, (w + 1) PERW)
+  static constexpr int NITEM = NDK + G::NBU + 1;
+  static constexpr int PERW = (NITEM + NLOAD - 1) / NLOAD;
   // ring slots: at most 4, as many as the LDS holds, and few enough that the
   // DMA instructions a loader keeps in flight fit the 6-bit vmcnt
-  static constexpr int PERW = NLOAD == 1 ? NDK + G::NBU + 1 : (NDK > G::NBU + 1 ? NDK : G::NBU + 1);
   static constexpr int DL = (LDS - HAND - XCH) / SLOT, DV = 2 + 63 / PERW;
   static constexpr int D0 = DL < DV ? (DL < 4 ? DL : 4) : (DV < 4 ? DV : 4);
   static constexpr int THREADS = 64 * (NREC + NLOAD + NOUT);
@@ -601,8 +607,7 @@ struct Carry {
   static constexpr bool PREF = D0 >= 3 && sizeof(IT) == sizeof(CT);
   static_assert(D0 >= 2 && D0 * SLOT + HAND + XCH <= LDS, "two ring slots fit the LDS");
   static_assert(G::NKX % NREC == 0 && G::NST % NREC == 0, "whole k-blocks per recurrence wave");
-  static_assert(NLOAD == 2 ? (D0 - 2) * NDK < 64 && (D0 - 2) * (G::NBU + 1) < 64
-                           : (D0 - 2) * (NDK + G::NBU + 1) < 64, "ring wait counts fit vmcnt");
+  static_assert((D0 - 2) * PERW < 64, "ring wait counts fit vmcnt");
   static_assert(KBYTES % 1024 == 0, "whole DMA instructions per chunk of keys");
 };
 
@@ -702,89 +707,120 @@ __device__ __forceinline__ typename Mma<CT>::frag query_frag(const IT* row, int 
   }
 }
 
-// Wave 1: the raw key rows of chunk c into `keys`.  DMA instruction q, lane l
-// writes slot bytes 1024 q + 16 l, i.e. row r = (1024 q + 16 l) / RB at
-// swizzled chunk pc; it reads logical chunk pc ^ kswz(r) of that row (rows
-// past the chunk's end repeat its last row, whose results are multiplied by
-// a zero row factor).  Without whole 16-byte rows (dk < DK or unaligned
-// rows) the rows are loaded element by element and stored with zeros past dk.
+// The raw key rows of chunk c element by element, for rows that are not
+// whole 16-byte vectors (dk < DK or unaligned rows): stored in the layout the
+// key DMA produces (below), with zeros past dk.
 template <class CT, class IT, int DK, bool VL>
-__device__ __forceinline__ void carry_keys(const ScanParams& p, const CarryCtx& x, char* keys, int c,
-                                           bool fast) {
+__device__ __forceinline__ void carry_keys_slow(const ScanParams& p, const CarryCtx& x, char* keys, int c) {
   typedef Carry<CT, IT, DK> K;
   int t0, n;
   chunk_at<VL>(p, (VL ? x.c0 : 0) + c, t0, n);
   const char* base = reinterpret_cast<const char*>(static_cast<const IT*>(p.k) + (int64_t)t0 * p.sqk +
                                                    (int64_t)x.hk * p.dk);
   const int64_t rowb = p.sqk * (int64_t)sizeof(IT);
-  if (fast) {
+  constexpr int VI = 16 / (int)sizeof(IT);
+  for (int q = 0; q < K::NDK; ++q) {
+    const int o = 1024 * q + 16 * x.lane, r = o / K::RB, pc = (o % K::RB) >> 4;
+    const int e0 = (pc ^ kswz<CT, K::NCH>(r)) * VI;
+    const IT* row = reinterpret_cast<const IT*>(base + min(r, n - 1) * rowb);
+    typename Vec16<IT>::type v;
 #pragma unroll
-    for (int q = 0; q < K::NDK; ++q) {
-      const int o = 1024 * q + 16 * x.lane, r = o / K::RB, pc = (o % K::RB) >> 4;
-      const int lc = pc ^ kswz<CT, K::NCH>(r);
-      dma_block(base + min(r, n - 1) * rowb + (lc << 4), keys + 1024 * q);
-    }
-  } else {
-    constexpr int VI = 16 / (int)sizeof(IT);
-    for (int q = 0; q < K::NDK; ++q) {
-      const int o = 1024 * q + 16 * x.lane, r = o / K::RB, pc = (o % K::RB) >> 4;
-      const int e0 = (pc ^ kswz<CT, K::NCH>(r)) * VI;
-      const IT* row = reinterpret_cast<const IT*>(base + min(r, n - 1) * rowb);
-      typename Vec16<IT>::type v;
-#pragma unroll
-      for (int i = 0; i < VI; ++i) v[i] = e0 + i < p.dk ? row[e0 + i] : IT(0);
-      *reinterpret_cast<typename Vec16<IT>::type*>(keys + o) = v;
-    }
+    for (int i = 0; i < VI; ++i) v[i] = e0 + i < p.dk ? row[e0 + i] : IT(0);
+    *reinterpret_cast<typename Vec16<IT>::type*>(keys + o) = v;
   }
 }
 
-// Wave 2: the U blocks and row scalars of chunk c into the slot.
-template <class CT, class IT, int DK, bool VL>
-__device__ __forceinline__ void carry_ublocks(const ScanParams& p, const CarryCtx& x, char* slot, int c) {
+// Loader LW: DMA items [LW PERW, (LW + 1) PERW) of each chunk into its ring
+// slot.  Items: the raw key rows' 1 KiB blocks q < NDK, then the U blocks,
+// then the row scalars.  Key block q, lane l writes slot bytes 1024 q + 16 l,
+// i.e. row r = (1024 q + 16 l) / RB at swizzled chunk pc, and reads logical
+// chunk pc ^ kswz(r) of that row (rows past the chunk's end repeat its last
+// row, whose results are multiplied by a zero row factor).  Without whole
+// 16-byte key rows (FAST false) loader 0 writes the keys with carry_keys_slow
+// instead: chunk i + 1 + PREF during chunk i (the recurrence reads chunk
+// i + 1's keys during chunk i when it prefetches), so they are published by
+// the barrier that ends chunk i - PREF.
+template <class CT, class IT, int DK, bool VL, int LW, bool FAST>
+__device__ __forceinline__ void carry_loader_w(const ScanParams& p, const CarryCtx& x, char* ring) {
   typedef Carry<CT, IT, DK> K;
-  const int64_t cg = (VL ? x.c0 : 0) + c;
-  const char* uf = static_cast<const char*>(p.Uf) + ((cg * p.Hv + x.h) * K::G::NBU * 64 + x.lane) * 16;
-  const char* sc = reinterpret_cast<const char*>(p.sc + (cg * p.Hv + x.h) * 256) + x.lane * 16;
-#pragma unroll
-  for (int b = 0; b < K::G::NBU; ++b) dma_block(uf + b * 1024, slot + K::UOFF + b * 1024);
-  dma_block(sc, slot + K::SOFF);
-}
-
-template <class CT, class IT, int DK, bool VL>
-__device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x, int lw, char* ring) {
-  typedef Carry<CT, IT, DK> K;
-  const bool fast = p.vec_qk && p.dk == DK;
-  const bool keys = K::NLOAD == 1 || lw == 0, ublocks = K::NLOAD == 1 || lw == 1;
-  // outstanding DMA instructions per chunk for this wave (fast key path)
-  constexpr int PER = K::NLOAD == 1 ? K::NDK + K::G::NBU + 1 : 0;
+  constexpr int NDK = K::NDK, NU = K::G::NBU;
+  constexpr int Q0 = LW * K::PERW < K::NITEM ? LW * K::PERW : K::NITEM;
+  constexpr int Q1 = Q0 + K::PERW < K::NITEM ? Q0 + K::PERW : K::NITEM;
+  constexpr int KQ0 = Q0 < NDK ? Q0 : NDK, KQ1 = Q1 < NDK ? Q1 : NDK;
+  // DMA instructions this wave issues per chunk (what its vmcnt waits count)
+  constexpr int PER = (Q1 - Q0) - (FAST ? 0 : KQ1 - KQ0);
+  constexpr int PREF = K::PREF ? 1 : 0;
   auto slot = [&](int c) { return ring + (c % K::D0) * K::SLOT; };
   auto issue = [&](int c) {
-    if (keys && fast) carry_keys<CT, IT, DK, VL>(p, x, slot(c), c, true);
-    if (ublocks) carry_ublocks<CT, IT, DK, VL>(p, x, slot(c), c);
+    char* s = slot(c);
+    const int64_t cg = (VL ? x.c0 : 0) + c;
+    if constexpr (FAST && KQ1 > KQ0) {
+      int t0, n;
+      chunk_at<VL>(p, cg, t0, n);
+      const char* base = reinterpret_cast<const char*>(static_cast<const IT*>(p.k) + (int64_t)t0 * p.sqk +
+                                                       (int64_t)x.hk * p.dk);
+      const int64_t rowb = p.sqk * (int64_t)sizeof(IT);
+#pragma unroll
+      for (int q = KQ0; q < KQ1; ++q) {
+        const int o = 1024 * q + 16 * x.lane, r = o / K::RB, pc = (o % K::RB) >> 4;
+        const int lc = pc ^ kswz<CT, K::NCH>(r);
+        dma_block(base + min(r, n - 1) * rowb + (lc << 4), s + 1024 * q);
+      }
+    }
+    if constexpr (Q1 > NDK) {
+      const char* uf = static_cast<const char*>(p.Uf) + ((cg * p.Hv + x.h) * NU * 64 + x.lane) * 16;
+#pragma unroll
+      for (int q = (Q0 > NDK ? Q0 : NDK); q < Q1; ++q) {
+        if (q < NDK + NU)
+          dma_block(uf + (q - NDK) * 1024, s + K::UOFF + (q - NDK) * 1024);
+        else
+          dma_block(reinterpret_cast<const char*>(p.sc + (cg * p.Hv + x.h) * 256) + x.lane * 16, s + K::SOFF);
+      }
+    }
   };
   for (int c = 0; c < K::D0 - 1; ++c)
     if (c < x.nchunks) issue(c);
-  if (keys && !fast) carry_keys<CT, IT, DK, VL>(p, x, slot(0), 0, false);
+  if constexpr (!FAST && LW == 0)
+    for (int c = 0; c <= PREF && c < x.nchunks; ++c) carry_keys_slow<CT, IT, DK, VL>(p, x, slot(c), c);
   wait_vmcnt<0>();
   lds_barrier();  // prologue
   for (int i = 0; i < x.nchunks; ++i) {
     if (i + K::D0 - 1 < x.nchunks) {
       issue(i + K::D0 - 1);
-      // chunk i+1 (prefetching recurrence: i+2) has landed
-      constexpr int AHEAD = K::D0 - 2 - (K::PREF ? 1 : 0);
-      if constexpr (K::NLOAD == 1)
-        wait_vmcnt<AHEAD * PER>();
-      else if (lw == 0)
-        wait_vmcnt<AHEAD * K::NDK>();
-      else
-        wait_vmcnt<AHEAD * (K::G::NBU + 1)>();
+      // chunk i+1 (prefetching recurrence: i+2) has landed: what may still
+      // be in flight is this wave's requests for the chunks after it
+      constexpr int AHEAD = K::D0 - 2 - PREF;
+      wait_vmcnt<AHEAD * PER>();
     } else {
       wait_vmcnt<0>();
     }
-    if (keys && !fast && i + 1 < x.nchunks) carry_keys<CT, IT, DK, VL>(p, x, slot(i + 1), i + 1, false);
+    if constexpr (!FAST && LW == 0)
+      if (i + 1 + PREF < x.nchunks) carry_keys_slow<CT, IT, DK, VL>(p, x, slot(i + 1 + PREF), i + 1 + PREF);
     lds_barrier();  // end of chunk i
   }
   lds_barrier();  // outputs of the last chunk
+}
+
+template <class CT, class IT, int DK, bool VL, int LW>
+__device__ __forceinline__ void carry_loader_fs(const ScanParams& p, const CarryCtx& x, char* ring) {
+  if (p.vec_qk && p.dk == DK)
+    carry_loader_w<CT, IT, DK, VL, LW, true>(p, x, ring);
+  else
+    carry_loader_w<CT, IT, DK, VL, LW, false>(p, x, ring);
+}
+
+template <class CT, class IT, int DK, bool VL>
+__device__ __forceinline__ void carry_loader(const ScanParams& p, const CarryCtx& x, int lw, char* ring) {
+  typedef Carry<CT, IT, DK> K;
+  static_assert(K::NLOAD >= 1 && K::NLOAD <= 3, "one to three loader waves");
+  static_assert(K::PERW * K::NLOAD >= K::NITEM && K::PERW * (K::NLOAD - 1) < K::NITEM, "items dealt to every loader");
+  if (lw == 0) carry_loader_fs<CT, IT, DK, VL, 0>(p, x, ring);
+  if constexpr (K::NLOAD > 1) {
+    if (lw == 1) carry_loader_fs<CT, IT, DK, VL, 1>(p, x, ring);
+  }
+  if constexpr (K::NLOAD > 2) {
+    if (lw == 2) carry_loader_fs<CT, IT, DK, VL, 2>(p, x, ring);
+  }
 }
 
 // Recurrence wave R of NREC: it holds the KPR k-blocks KB0 = R KPR.. of the

@@ -135,6 +135,22 @@ def test_scan_gqa_initial_state_and_f16_io(clef, precision):
 
 
 @gpu
+@pytest.mark.parametrize("precision,dtype,dk", [("mixed", torch.float16, 100), ("mixed", torch.float32, 100),
+                                                ("strict", torch.float32, 48), ("strict", torch.float32, 20)])
+def test_scan_key_rows_loaded_element_wise_over_many_chunks(clef, precision, dtype, dk):
+    """dk below the padded key width: the carry loads the raw key rows element
+    by element instead of by DMA.  Eleven chunks, so the ring wraps, and with
+    f16 keys under f16 products or f32 under f32 the recurrence reads each
+    chunk's keys one chunk early (written two chunks ahead by the loader)."""
+    T, Hk, Hv, dv = 700, 2, 4, 32
+    q, k, v, g, beta = case_inputs(23, T, Hk, Hv, dk, dv, dtype=dtype)
+    out, _, final = clef.DeltaScan(dk, dv, precision).prefill(q, k, v, g, beta)
+    eo, _, ef = oracle.delta_scan(*_np(q, k, v, g, beta))
+    _check(out.cpu().numpy(), eo, precision)
+    _check(final.cpu().numpy(), ef, precision)
+
+
+@gpu
 def test_scan_strided_views_of_packed_projection(clef):
     """q,k,v as views into one [T, 2*Hk*dk + Hv*dv] row (the conv output layout)."""
     T, Hk, Hv, dk, dv = 130, 2, 4, 64, 64
