@@ -22,6 +22,20 @@
 #include "gemm.hpp"
 
 namespace clef {
+
+// CUs of the current device (cached per device)
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 namespace {
 
 constexpr int kBM = 256, kBK = 64;  // largest row tile, K stage
@@ -53,7 +67,7 @@ __device__ __forceinline__ void vm_wait_n(int n, std::integer_sequence<int, Ns..
 __device__ __forceinline__ void vm_wait_n(int n) { vm_wait_n(n, std::make_integer_sequence<int, 40>{}); }
 
 
-template <int BM, int BN, int VM, int NSA, int NSB, int EPI>
+template <int BM, int BN, int VM, int NSA, int NSB, int EPI, bool PERSIST>
 __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int kWaves = VM * 2;  // VM wave rows x 2 wave columns
   constexpr int WM = BM / VM, WN = BN / 2;
@@ -75,21 +89,23 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- tile index with XCD-compact placement (as gemm.hip)
+  // ---- tile index with XCD-compact placement (as gemm.hip).  A persistent
+  // launch (one work-group per CU, gridDim.x a multiple of 8) takes the tiles
+  // blockIdx.x, blockIdx.x + gridDim.x, ..., which stay on its XCD.
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN);
   const int ntiles = tiles_m * tiles_n;
-  int t = blockIdx.x;
-  if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
-  const int group = 4;
-  const int gsize = group * tiles_n;
-  const int gid = t / gsize;
-  const int first_m = gid * group;
-  const int gm = min(group, tiles_m - first_m);
-  const int tm = first_m + (t % gsize) % gm;
-  const int tn = (t % gsize) / gm;
-  const int m0 = tm * BM;
-  const int n0 = tn * (EPI == 2 ? BN / 2 : BN);
+  auto coords = [&](int t, int& tm0, int& tn0) {
+    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    const int group = 4;
+    const int gsize = group * tiles_n;
+    const int first_m = (t / gsize) * group;
+    const int gm = min(group, tiles_m - first_m);
+    tm0 = (first_m + (t % gsize) % gm) * BM;
+    tn0 = ((t % gsize) / gm) * (EPI == 2 ? BN / 2 : BN);
+  };
+  int tile = blockIdx.x, m0 = 0, n0 = 0;
+  coords(tile, m0, n0);
 
   const half_t* X = static_cast<const half_t*>(p.x);
   const half_t* W = static_cast<const half_t*>(p.w);
@@ -105,15 +121,15 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
 #pragma unroll
   for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
   const int lrow = lane >> 3;
-  // (part / nparts: the instructions q with q % nparts == part, so a stage's
-  // DMA can be spread over the k-blocks of the stage before it; a null sa or
-  // sb skips that operand)
-  auto issue = [&](half_t* sa, half_t* sb, int k0, int part = 0, int nparts = 1) {
+  // (tile origin tm0, tn0; part / nparts: the instructions q with
+  // q % nparts == part, so a stage's DMA can be spread over the k-blocks of
+  // the stage before it; a null sa or sb skips that operand)
+  auto issue = [&](half_t* sa, half_t* sb, int k0, int tm0, int tn0, int part = 0, int nparts = 1) {
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       if (q % nparts != part || !sa) continue;
       const int j = wave * NA + q;
-      const int row = min(m0 + 8 * j + lrow, p.M - 1);
+      const int row = min(tm0 + 8 * j + lrow, p.M - 1);
       dma16(X + row * (int)p.ldx + lcol[j & 1] + k0, sa + j * 512);
     }
 #pragma unroll
@@ -124,22 +140,16 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       const half_t* src;
       if (EPI == 2) {  // wave column wb holds [gate | up] rows of the same outputs
         const int wb = row / WN, within = row % WN;
-        const int nr = min(n0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
+        const int nr = min(tn0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
         src = (within >= WN / 2 ? W2 : W) + (int64_t)nr * p.ldw;
       } else {
-        src = W + (int64_t)min(n0 + row, p.N - 1) * p.ldw;
+        src = W + (int64_t)min(tn0 + row, p.N - 1) * p.ldw;
       }
       dma16(src + lcol[j & 1] + k0, sb + j * 512);
     }
   };
 
   float16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   // fragment reads: row r = (wave offset) + 32 i + lane % 32 has swizzle key
   // (lane % 32 >> 1) & 7, so a lane's byte offset within any 32-row block is
@@ -192,11 +202,14 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   // order, so what may stay in flight at that wait is what was issued after
   // stage kt+1's last request: stage kt+2 of each three-slot operand (with
   // NSA = 2, NSB = 3 the A stage kt+1 is issued before the B stage kt+2).
+  // A persistent work-group requests the next tile's first stages during
+  // the last stages of the current one, so the ring runs on across tiles
+  // (`next`: the next tile's stages were requested).
   constexpr int KEEP = (NSA == 3 ? NA : 0) + (NSB == 3 ? NB : 0);
   const int nk = p.K / kBK;
-  auto wait_next = [&](int kt) {  // before the barrier that publishes stage kt+1
+  auto wait_next = [&](int kt, bool next) {  // before the barrier that publishes stage kt+1
     if constexpr (KEEP > 0) {
-      if (kt + 2 < nk) {
+      if (kt + 2 < nk || next) {
         vm_wait<KEEP>();
         return;
       }
@@ -205,10 +218,10 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   };
 #pragma unroll
   for (int st = 0; st < NSB - 1; ++st) {
-    if (st < NSA - 1 && st < nk) issue(sA(st), nullptr, st * kBK);
-    if (st < nk) issue(nullptr, sB(st), st * kBK);
+    if (st < NSA - 1 && st < nk) issue(sA(st), nullptr, st * kBK, m0, n0);
+    if (st < nk) issue(nullptr, sB(st), st * kBK, m0, n0);
   }
-  wait_next(-1);
+  wait_next(-1, false);
   lds_barrier();
 
   // Residual tiles (EPI 1, 128-wide) are read into registers over the last
@@ -224,7 +237,6 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   static_assert(!PF || NR % kPD == 0, "prefetch batches");
   const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
   const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
-  const bool pf = PF && yvec && nk >= kPD && m0 + BM <= p.M && n0 + BN <= p.N;
   float4 pre[PF ? NR : 1];
   auto prefetch = [&](int b) {
 #pragma unroll
@@ -236,147 +248,223 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   };
 
   int ca = 0, cb = 0;
-  auto stage = [&](int kt) {
-    const int na = ca == 0 ? NSA - 1 : ca - 1;  // (ca + NSA - 1) % NSA
-    const int nb = cb == 0 ? NSB - 1 : cb - 1;
-    const bool more_a = kt + NSA - 1 < nk, more_b = kt + NSB - 1 < nk;
-    compute(sA(ca), sB(cb), [&](int kb) {
-      if constexpr (NSA == NSB) {
-        // the next stage's DMA, half before each of the first two k-blocks'
-        // products (whole prefill 0.7% faster than all of it at the stage
-        // start, by interleaved A/B; spread over all four k-blocks, the last
-        // quarter has too little time to land when the weights come from HBM:
-        // 2% slower)
-        if (more_a && kb < 2) issue(sA(na), sB(nb), (kt + NSA - 1) * kBK, kb, 2);
-      } else {
-        // A one stage ahead before k-block 0, B two stages ahead before
-        // k-block 1 (in that order: see wait_next)
-        if (more_a && kb == 0) issue(sA(na), nullptr, (kt + NSA - 1) * kBK);
-        if (more_b && kb == 1) issue(nullptr, sB(nb), (kt + NSB - 1) * kBK);
-      }
-    });
-  };
-  auto advance = [&]() {
-    ca = ca + 1 == NSA ? 0 : ca + 1;
-    cb = cb + 1 == NSB ? 0 : cb + 1;
-  };
-  const int kmain = pf ? nk - kPD : nk;
-  for (int kt = 0; kt < kmain; ++kt) {
-    stage(kt);
-    wait_next(kt);
-    lds_barrier();
-    advance();
-  }
-  if constexpr (PF) {
-    if (pf) {
+  for (;;) {  // the tiles of this work-group
+    const int ntile = tile + gridDim.x;
+    const bool next = PERSIST && ntile < ntiles;
+    int nm0 = 0, nn0 = 0;
+    if (next) coords(ntile, nm0, nn0);
+    const bool pf = PF && yvec && nk >= kPD && m0 + BM <= p.M && n0 + BN <= p.N;
 #pragma unroll
-      for (int d = 0; d < kPD; ++d) {
-        stage(nk - kPD + d);
-        prefetch(d);
-        // issued after stage kt+1's last request: batch d-1, stage kt+2's
-        // DMA (NSA = NSB = 3 here) and batch d
-        vm_wait_n((d >= 1 ? NRB : 0) + (d + 2 < kPD ? NA + NB : 0) + NRB);
-        lds_barrier();
-        advance();
-      }
-    }
-  }
-
-  // ---- epilogue.  The loop's last barrier follows every wave's last
-  // fragment read, so each wave now owns a 32 x WN f32 staging block.
-  // acc[i][j][e] holds row (e/4)*8 + (lane/32)*4 + e%4, column lane%32 of
-  // 32 x 32 block (i, j); a 32-row slab is written there and read back as
-  // 4-column chunks, so the global accesses are 8- or 16-byte vectors along
-  // the rows.  (LDS operations of one wave complete in order, so the
-  // write -> read -> next write sequence needs no barrier.)
-  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
-  const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = acc[i][j][e];
-    const int rbase = m0 + wm * WM + i * 32;
-    const int cbase = n0 + wn * OW;
-    float4 v[PER], res[PER];
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
-      if (EPI == 2) {
-        const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
-        const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
-        // half roundings of neural.metal:35-42; SiLU on the hardware exp2 and
-        // reciprocal (expf and an IEEE division cost ~1.8% of a prefill
-        // here), the same function as clef_silu_mul's, so fused and unfused
-        // agree bit for bit (neural.rs:484-492)
-        auto sw = [](float gv, float uv) {
-          const float gh = static_cast<float>(to_f16(gv));
-          const float sh = static_cast<float>(to_f16(silu_hw(gh)));
-          return sh * static_cast<float>(to_f16(uv));
-        };
-        v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
-      } else {
-        v[q] = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
-      }
-    }
-    if (EPI == 1) {
-      // residual reads all issued before the first store (or made during
-      // the last stages)
-#pragma unroll
-      for (int q = 0; q < PER; ++q) {
-        if (PF && pf) {
-          res[q] = pre[PF ? i * PER + q : 0];
-          continue;
-        }
-        const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
-        const float* src = static_cast<const float*>(p.y) + (int64_t)r * p.ldy + c;
-        if (yvec && r < p.M && c + 3 < p.N) {
-          res[q] = *reinterpret_cast<const float4*>(src);
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    // requests stage ks of this tile or, past its end, of the next one
+    auto issue_at = [&](half_t* sa, half_t* sb, int ks, int part = 0, int nparts = 1) {
+      if (ks < nk)
+        issue(sa, sb, ks * kBK, m0, n0, part, nparts);
+      else if (next)
+        issue(sa, sb, (ks - nk) * kBK, nm0, nn0, part, nparts);
+    };
+    auto stage = [&](int kt) {
+      const int na = ca == 0 ? NSA - 1 : ca - 1;  // (ca + NSA - 1) % NSA
+      const int nb = cb == 0 ? NSB - 1 : cb - 1;
+      compute(sA(ca), sB(cb), [&](int kb) {
+        if constexpr (NSA == NSB) {
+          // the next stage's DMA, half before each of the first two k-blocks'
+          // products (whole prefill 0.7% faster than all of it at the stage
+          // start, by interleaved A/B; spread over all four k-blocks, the last
+          // quarter has too little time to land when the weights come from HBM:
+          // 2% slower)
+          if (kb < 2) issue_at(sA(na), sB(nb), kt + NSA - 1, kb, 2);
         } else {
-          res[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (r < p.M) {
-            if (c < p.N) res[q].x = src[0];
-            if (c + 1 < p.N) res[q].y = src[1];
-            if (c + 2 < p.N) res[q].z = src[2];
-            if (c + 3 < p.N) res[q].w = src[3];
+          // A one stage ahead before k-block 0, B two stages ahead before
+          // k-block 1 (in that order: see wait_next)
+          if (kb == 0) issue_at(sA(na), nullptr, kt + NSA - 1);
+          if (kb == 1) issue_at(nullptr, sB(nb), kt + NSB - 1);
+        }
+      });
+    };
+    auto advance = [&]() {
+      ca = ca + 1 == NSA ? 0 : ca + 1;
+      cb = cb + 1 == NSB ? 0 : cb + 1;
+    };
+    const int kmain = pf ? nk - kPD : nk;
+    for (int kt = 0; kt < kmain; ++kt) {
+      stage(kt);
+      wait_next(kt, next);
+      lds_barrier();
+      advance();
+    }
+    if constexpr (PF) {
+      if (pf) {
+#pragma unroll
+        for (int d = 0; d < kPD; ++d) {
+          stage(nk - kPD + d);
+          prefetch(d);
+          // issued after stage kt+1's last request: batch d-1, stage kt+2's
+          // DMA (NSA = NSB = 3 here) and batch d
+          vm_wait_n((d >= 1 ? NRB : 0) + (d + 2 < kPD ? NA + NB : 0) + NRB);
+          lds_barrier();
+          advance();
+        }
+      }
+    }
+
+    if constexpr (PERSIST) {
+      // ---- epilogue of a persistent work-group.  The next tile's first
+      // stages are in flight into the other slots; the slots of this tile's
+      // last stage are free, and each wave stages a 32 x WN slab in f16 there
+      // (waves 0-3 in the A slot, 4-7 in the B slot).  Values are rounded to
+      // f16 once, as the stores would round them (EPI 0), or as SwiGLU rounds
+      // gate and up before combining them (neural.metal:35-42).
+      static_assert(EPI != 1 && kWaves == 8 && 4 * 32 * WN <= kStA && 4 * 32 * WN <= kStB,
+                    "f16 staging of four waves fits a stage slot");
+      const int pa = ca == 0 ? NSA - 1 : ca - 1, pb = cb == 0 ? NSB - 1 : cb - 1;
+      half_t* const stg = (wave < 4 ? sA(pa) : sB(pb)) + (wave & 3) * (32 * WN);
+      const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = to_f16(acc[i][j][e]);
+        const int rbase = m0 + wm * WM + i * 32;
+        const int cbase = n0 + wn * OW;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
+          half4 h = *reinterpret_cast<const half4*>(stg + row * WN + c4 * 4);
+          if constexpr (EPI == 2) {
+            const half4 u = *reinterpret_cast<const half4*>(stg + row * WN + OW + c4 * 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              // the same function as clef_silu_mul's (neural.rs:484-492)
+              const float sh = static_cast<float>(to_f16(silu_hw(static_cast<float>(h[t]))));
+              h[t] = static_cast<half_t>(sh * static_cast<float>(u[t]));
+            }
+          }
+          const int r = rbase + row, c = cbase + c4 * 4;
+          if (r >= p.M) continue;
+          half_t* dst = static_cast<half_t*>(p.y) + (int64_t)r * p.ldy + c;
+          if (yvec && c + 3 < p.N) {
+            *reinterpret_cast<half4*>(dst) = h;
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (c + t < p.N) dst[t] = h[t];
+          }
+        }
+      }
+      if (!next) break;
+      // every wave's staging reads are done before the next tile's DMA
+      // (stage 0) refills these slots
+      lds_barrier();
+      tile = ntile;
+      m0 = nm0;
+      n0 = nn0;
+      continue;
+    }
+
+    // ---- epilogue.  The loop's last barrier follows every wave's last
+    // fragment read, so each wave now owns a 32 x WN f32 staging block.
+    // acc[i][j][e] holds row (e/4)*8 + (lane/32)*4 + e%4, column lane%32 of
+    // 32 x 32 block (i, j); a 32-row slab is written there and read back as
+    // 4-column chunks, so the global accesses are 8- or 16-byte vectors along
+    // the rows.  (LDS operations of one wave complete in order, so the
+    // write -> read -> next write sequence needs no barrier.)
+    float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
+    const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+  #pragma unroll
+    for (int i = 0; i < TM; ++i) {
+  #pragma unroll
+      for (int j = 0; j < TN; ++j)
+  #pragma unroll
+        for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = acc[i][j][e];
+      const int rbase = m0 + wm * WM + i * 32;
+      const int cbase = n0 + wn * OW;
+      float4 v[PER], res[PER];
+  #pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
+        if (EPI == 2) {
+          const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+          const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
+          // half roundings of neural.metal:35-42; SiLU on the hardware exp2 and
+          // reciprocal (expf and an IEEE division cost ~1.8% of a prefill
+          // here), the same function as clef_silu_mul's, so fused and unfused
+          // agree bit for bit (neural.rs:484-492)
+          auto sw = [](float gv, float uv) {
+            const float gh = static_cast<float>(to_f16(gv));
+            const float sh = static_cast<float>(to_f16(silu_hw(gh)));
+            return sh * static_cast<float>(to_f16(uv));
+          };
+          v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
+        } else {
+          v[q] = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+        }
+      }
+      if (EPI == 1) {
+        // residual reads all issued before the first store (or made during
+        // the last stages)
+  #pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          if (PF && pf) {
+            res[q] = pre[PF ? i * PER + q : 0];
+            continue;
+          }
+          const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
+          const float* src = static_cast<const float*>(p.y) + (int64_t)r * p.ldy + c;
+          if (yvec && r < p.M && c + 3 < p.N) {
+            res[q] = *reinterpret_cast<const float4*>(src);
+          } else {
+            res[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < p.M) {
+              if (c < p.N) res[q].x = src[0];
+              if (c + 1 < p.N) res[q].y = src[1];
+              if (c + 2 < p.N) res[q].z = src[2];
+              if (c + 3 < p.N) res[q].w = src[3];
+            }
+          }
+        }
+      }
+  #pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
+        if (r >= p.M) continue;
+        float4 o = v[q];
+        if (EPI == 1) {
+          auto rd = [&](float x) { return p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(x)) : x; };
+          o = make_float4(res[q].x + rd(o.x), res[q].y + rd(o.y), res[q].z + rd(o.z), res[q].w + rd(o.w));
+        }
+        const int64_t off = (int64_t)r * p.ldy + c;
+        if (esz == 2) {
+          half_t* dst = static_cast<half_t*>(p.y) + off;
+          const half_t h[4] = {static_cast<half_t>(o.x), static_cast<half_t>(o.y), static_cast<half_t>(o.z),
+                               static_cast<half_t>(o.w)};
+          if (yvec && c + 3 < p.N) {
+            *reinterpret_cast<half4*>(dst) = half4{h[0], h[1], h[2], h[3]};
+          } else {
+  #pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (c + t < p.N) dst[t] = h[t];
+          }
+        } else {
+          float* dst = static_cast<float*>(p.y) + off;
+          if (yvec && c + 3 < p.N) {
+            *reinterpret_cast<float4*>(dst) = o;
+          } else {
+            const float f[4] = {o.x, o.y, o.z, o.w};
+  #pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (c + t < p.N) dst[t] = f[t];
           }
         }
       }
     }
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
-      if (r >= p.M) continue;
-      float4 o = v[q];
-      if (EPI == 1) {
-        auto rd = [&](float x) { return p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(x)) : x; };
-        o = make_float4(res[q].x + rd(o.x), res[q].y + rd(o.y), res[q].z + rd(o.z), res[q].w + rd(o.w));
-      }
-      const int64_t off = (int64_t)r * p.ldy + c;
-      if (esz == 2) {
-        half_t* dst = static_cast<half_t*>(p.y) + off;
-        const half_t h[4] = {static_cast<half_t>(o.x), static_cast<half_t>(o.y), static_cast<half_t>(o.z),
-                             static_cast<half_t>(o.w)};
-        if (yvec && c + 3 < p.N) {
-          *reinterpret_cast<half4*>(dst) = half4{h[0], h[1], h[2], h[3]};
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            if (c + t < p.N) dst[t] = h[t];
-        }
-      } else {
-        float* dst = static_cast<float*>(p.y) + off;
-        if (yvec && c + 3 < p.N) {
-          *reinterpret_cast<float4*>(dst) = o;
-        } else {
-          const float f[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            if (c + t < p.N) dst[t] = f[t];
-        }
-      }
-    }
+
+    break;
   }
 }
 
@@ -391,7 +479,19 @@ int launch(const GemmParams& p, hipStream_t s) {
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
   constexpr int VM = 4;  // 8 waves, two per SIMD (WM = BM / 4 rows each)
-  hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI>), dim3(tiles_m * tiles_n), dim3(VM * 128), 0, s, p);
+  const int ntiles = tiles_m * tiles_n, cus = device_cus();
+  // More tiles than CUs: one persistent work-group per CU runs its tiles
+  // back to back, requesting the next tile's first stages during the last
+  // stages of the current one (no prologue wait, no gap between work-groups).
+  // It stages the epilogue in f16 in the freed slots: 256- and 192-wide
+  // tiles (two activation slots), f16 output, the store and SwiGLU epilogues.
+  if constexpr (NSA == 2 && EPI != 1) {
+    if (p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2) {
+      hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, true>), dim3(cus), dim3(VM * 128), 0, s, p);
+      return check_launch("gemm");
+    }
+  }
+  hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, false>), dim3(ntiles), dim3(VM * 128), 0, s, p);
   return check_launch("gemm");
 }
 
@@ -538,18 +638,6 @@ bool gemm_f16_dma_ok(const GemmParams& p) {
          (int64_t)p.M * p.ldx < (int64_t(1) << 31);
 }
 
-// CUs of the current device (cached per device)
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 // Tile shape: one tile per CU at a time (the LDS holds one), so a launch
 // takes ceil(tiles / CUs) rounds, each as long as a tile; a smaller tile

@@ -63,6 +63,31 @@ def test_gemm_projection_shapes(clef, N, dtype):
 
 
 @gpu
+@pytest.mark.parametrize("M,N,K", [(2100, 12300, 128), (2100, 12300, 2048), (2048, 9216, 2048), (4096, 12288, 192)])
+def test_gemm_persistent_launches(clef, M, N, K):
+    """More tiles than CUs: one work-group per CU runs several tiles, the
+    next tile's first stages requested during the current one's last.
+    Ragged rows and columns, two K stages, a partial last round, 192-wide
+    tiles; the f32 output (one tile per work-group) must agree bit for bit
+    once rounded."""
+    x, w = _inputs(9, M, N, K, torch.float16)
+    y = clef.gemm(x, w)
+    _check_f16(y, x, w)
+    assert torch.equal(clef.gemm(x, w, out_dtype=torch.float32).half(), y)
+
+
+@gpu
+@pytest.mark.parametrize("M,N,K", [(2100, 6150, 128), (2048, 6144, 2048)])
+def test_swiglu_persistent_launches(clef, M, N, K):
+    gen = torch.Generator(device="cuda").manual_seed(15)
+    x = torch.randn((M, K), generator=gen, device="cuda").half()
+    wg = (torch.randn((N, K), generator=gen, device="cuda") * 0.05).half()
+    wu = (torch.randn((N, K), generator=gen, device="cuda") * 0.05).half()
+    y = clef.gemm_swiglu(x, wg, wu)
+    assert torch.equal(y, clef.silu_mul(clef.gemm(x, wg), clef.gemm(x, wu)))
+
+
+@gpu
 @pytest.mark.parametrize("M,N,K", [(4096, 2048, 4096), (4096, 2048, 6144), (20, 16, 8), (300, 203, 128),
                                    (4096, 3000, 256),
                                    # residual tiles read during the last eight K stages: full and
