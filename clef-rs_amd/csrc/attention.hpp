@@ -21,7 +21,6 @@ struct AttnParams {
   const int* cu_q;   // [nseq + 1] (device)
   int2* pairs;       // [blocks / heads] {sequence, query tile}, most keys first
   int* npairs;       // valid entries of pairs
-  int* keys;         // [tiles] key count per query tile (table scratch)
   int* spans;        // [nseq + 1] cu_q made monotone in [0, T] (ragged.hpp)
   int nseq;
   const void* pk;    // [kvh][ldpk][d] or null

@@ -750,9 +750,9 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
 // count (most first, ties in sequence order) for a longest-first launch;
 // beyond 8192 tiles in sequence order.  Any offset table keeps the pair
 // table inside its T/128 + nseq entries.
-__global__ __launch_bounds__(kTabThreads) void attn_tables(const int* __restrict__ cu, int nseq, int T, int np,
+__global__ __launch_bounds__(kTabThreads) void attn_tables(const int* __restrict__ cu, int nseq, int T,
                                                            int* __restrict__ spans, int2* __restrict__ pairs,
-                                                           int* __restrict__ npairs, int* __restrict__ keys) {
+                                                           int* __restrict__ npairs) {
   __shared__ int s_part[kTabThreads];
   __shared__ int s_R[kMaxRaggedSeq + 1];
   __shared__ int s_total;
@@ -770,10 +770,7 @@ __global__ __launch_bounds__(kTabThreads) void attn_tables(const int* __restrict
   rg_count_5(g, tid, &s_total);
   __syncthreads();
   if (tid == 0) *npairs = s_total;
-  rg_attn_6(g, tid, 128, np, keys);
-  __threadfence_block();
-  __syncthreads();
-  rg_attn_7(g, tid, 128, s_total, keys, reinterpret_cast<int*>(pairs));
+  rg_attn_6(g, tid, 128, s_total, reinterpret_cast<int*>(pairs));
 }
 
 // work-groups resident at once (CUs x occupancy of the instance), per device
@@ -836,7 +833,7 @@ size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t attn_tables_bytes(int T, int nseq) {
   const size_t tiles = (size_t)(T + 127) / 128 + nseq;
-  return al256(tiles * sizeof(int2)) + al256(tiles * sizeof(int)) + 256 + al256(((size_t)nseq + 1) * sizeof(int));
+  return al256(tiles * sizeof(int2)) + 256 + al256(((size_t)nseq + 1) * sizeof(int));
 }
 
 void attn_carve_tables(AttnParams& p, void* ws) {
@@ -844,16 +841,14 @@ void attn_carve_tables(AttnParams& p, void* ws) {
   char* b = static_cast<char*>(ws);
   p.pairs = reinterpret_cast<int2*>(b);
   b += al256(tiles * sizeof(int2));
-  p.keys = reinterpret_cast<int*>(b);
-  b += al256(tiles * sizeof(int));
   p.npairs = reinterpret_cast<int*>(b);
   p.spans = reinterpret_cast<int*>(b + 256);
 }
 
 int attn_f16_tables(AttnParams& p, hipStream_t s) {
   if (p.nseq < 1 || p.nseq > kMaxRaggedSeq) return fail(-1, "attention: 1..4096 sequences");
-  hipLaunchKernelGGL(attn_tables, dim3(1), dim3(kTabThreads), 0, s, p.cu_q, p.nseq, p.qn, p.np, p.spans, p.pairs,
-                     p.npairs, p.keys);
+  hipLaunchKernelGGL(attn_tables, dim3(1), dim3(kTabThreads), 0, s, p.cu_q, p.nseq, p.qn, p.spans, p.pairs,
+                     p.npairs);
   if (int rc = check_launch("attention tables")) return rc;
   p.cu_q = p.spans;  // the attention kernel reads the monotone spans
   return 0;

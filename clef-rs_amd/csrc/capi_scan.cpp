@@ -204,7 +204,7 @@ extern "C" int clef_ragged_plan(const int32_t* cu_seqlens, int nseq, int T, int 
   CLEF_REQUIRE(unit == 64 || unit == 128, "ragged plan: unit 64 (scan chunks) or 128 (attention query tiles)");
   const size_t cap = (size_t)(T + unit - 1) / unit + nseq;
   CLEF_REQUIRE(!table || table_entries >= cap, "ragged plan: table smaller than ceil(T / unit) + nseq entries");
-  std::vector<int> part(kTabThreads), R(nseq + 1), stab(4 * (size_t)nseq), ctab(2 * cap), keys(cap);
+  std::vector<int> part(kTabThreads), R(nseq + 1), stab(4 * (size_t)nseq), ctab(2 * cap);
   const Ragged g{cu_seqlens, nseq, T, part.data(), R.data()};
   int total = 0;
   for (int t = 0; t < kTabThreads; ++t) rg_spans_1(g, t);
@@ -216,8 +216,7 @@ extern "C" int clef_ragged_plan(const int32_t* cu_seqlens, int nseq, int T, int 
   if (unit == 64) {
     for (int t = 0; t < kTabThreads; ++t) rg_scan_6(g, t, unit, ctab.data(), stab.data());
   } else {
-    for (int t = 0; t < kTabThreads; ++t) rg_attn_6(g, t, unit, 0, keys.data());
-    for (int t = 0; t < kTabThreads; ++t) rg_attn_7(g, t, unit, total, keys.data(), ctab.data());
+    for (int t = 0; t < kTabThreads; ++t) rg_attn_6(g, t, unit, total, ctab.data());
   }
   for (int j = 0; j <= nseq; ++j) spans[j] = R[j];
   if (table)

@@ -114,34 +114,34 @@ __host__ __device__ inline void rg_scan_6(const Ragged& g, int tid, int chunk, i
   }
 }
 
-// Attention, step 6: the key count of each query tile (prefix + the causal
-// reach of its last query).
-__host__ __device__ inline void rg_attn_6(const Ragged& g, int tid, int tile, int np, int* keys) {
+// Attention, step 6: (sequence, tile) pairs ranked by key count (most
+// first, ties in table order); beyond 8192 tiles in table order.  Query tile
+// t of sequence s sees np + min(tile (t + 1), len_s) keys; np is common to
+// all tiles, so the order is that of m = min(tile (t + 1), len_s).  A
+// sequence's m values are tile, 2 tile, ..., tile (n_s - 1), len_s, rising,
+// so how many of them exceed m, and whether one equals m, are closed forms:
+// a tile's rank costs one pass over the sequences.
+__host__ __device__ inline int rg_tiles_above(int len, int nt, int m, int tile) {
+  return len > m ? rg_max(0, nt - m / tile) : 0;
+}
+__host__ __device__ inline bool rg_tile_at(int len, int m, int tile) {
+  return len > 0 && (m == len || (m % tile == 0 && m < len));
+}
+__host__ __device__ inline void rg_attn_6(const Ragged& g, int tid, int tile, int total, int* pairs) {
   int s0, s1;
   rg_range(tid, g.nseq, s0, s1);
   int f = g.part[tid];
   for (int s = s0; s < s1; ++s) {
     const int len = g.R[s + 1] - g.R[s], nt = rg_units(g, s, tile);
-    for (int t = 0; t < nt; ++t) keys[f + t] = np + rg_min(tile * (t + 1), len);
-    f += nt;
-  }
-}
-// Attention, step 7: (sequence, tile) pairs ranked by key count (most first,
-// ties in table order); beyond 8192 tiles in table order.
-__host__ __device__ inline void rg_attn_7(const Ragged& g, int tid, int tile, int total, const int* keys,
-                                          int* pairs) {
-  int s0, s1;
-  rg_range(tid, g.nseq, s0, s1);
-  int f = g.part[tid];
-  for (int s = s0; s < s1; ++s) {
-    const int nt = rg_units(g, s, tile);
     for (int t = 0; t < nt; ++t) {
-      const int i = f + t;
-      int rank = i;
+      int rank = f + t;
       if (total <= 8192) {
+        const int m = rg_min(tile * (t + 1), len);
         rank = 0;
-        const int ki = keys[i];
-        for (int j = 0; j < total; ++j) rank += (keys[j] > ki) || (keys[j] == ki && j < i);
+        for (int j = 0; j < g.nseq; ++j) {
+          const int lj = g.R[j + 1] - g.R[j];
+          rank += rg_tiles_above(lj, (lj + tile - 1) / tile, m, tile) + (j < s && rg_tile_at(lj, m, tile));
+        }
       }
       pairs[2 * rank] = s;
       pairs[2 * rank + 1] = t;

@@ -139,6 +139,52 @@ def test_ragged_plan_malformed_tables_stay_in_bounds(clef, unit, cu, T):
     _check_plan(clef, cu, T, unit)
 
 
+def _brute_attention_order(spans):
+    """(sequence, tile) pairs in the attention launch order, from its
+    definition: key count np + min(128 (t + 1), len) per query tile, most
+    first, ties in table order; beyond 8192 tiles, table order."""
+    import numpy as np
+    lens = np.diff(np.asarray(spans, np.int64))
+    items = [(s, t, min(128 * (t + 1), int(lens[s]))) for s in range(len(lens))
+             for t in range((int(lens[s]) + 127) // 128)]
+    if len(items) <= 8192:
+        items = [it for _, it in sorted(enumerate(items), key=lambda e: (-e[1][2], e[0]))]
+    return np.array([(s, t) for s, t, _ in items], np.int64).reshape(-1, 2)
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_ragged_plan_attention_order_matches_definition(clef, case):
+    """The closed-form ranks (counts of each sequence's tiles above a key
+    count, and ties in earlier sequences) against a sort by key count."""
+    import numpy as np
+    rng = np.random.default_rng(40 + case)
+    if case == 0:    # uniform lengths, many ties at multiples of 128
+        lens = rng.integers(1, 9, 50) * 128
+    elif case == 1:  # random lengths
+        lens = rng.integers(1, 3000, 64)
+    elif case == 2:  # near-multiples of 128, single tokens, empty sequences
+        lens = rng.choice([0, 1, 127, 128, 129, 255, 256, 257, 4096], 200)
+    elif case == 3:  # a 512-token prefix's ragged batch: 32 requests in [128, 4096]
+        lens = rng.integers(128, 4097, 32)
+    elif case == 4:  # 4096 sequences of 256: exactly 8192 tiles, ranked
+        lens = np.full(4096, 256)
+    else:            # past 8192 tiles (3000 x 3): table order
+        lens = np.full(3000, 300)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    T = max(int(cu[-1]), 1)
+    spans, units = clef.ragged_plan(cu, T, 128)
+    expected = _brute_attention_order(spans)
+    assert units.shape == expected.shape and (units == expected).all()
+
+
+@pytest.mark.parametrize("cu,T", [([0, 1000, 0, 1000, 0, 1000], 1000), ([-50, 100, 40, 900, 300, 1000], 1000),
+                                  ([0, 5000, 6000], 1000)])
+def test_ragged_plan_attention_order_of_malformed_tables(clef, cu, T):
+    spans, units = clef.ragged_plan(cu, T, 128)
+    expected = _brute_attention_order(spans)
+    assert units.shape == expected.shape and (units == expected).all()
+
+
 def test_ragged_plan_rejects_bad_arguments(clef):
     import numpy as np
     cu = np.array([0, 10], np.int32)
