@@ -194,19 +194,6 @@ __device__ __forceinline__ bool chunk_span(const ScanParams& p, int c, int& t0, 
   return true;
 }
 
-// Token span of chunk c in the carry, with the batch kind known at compile
-// time (one sequence: no table lookups on the recurrence's path).
-template <bool VL>
-__device__ __forceinline__ void chunk_at(const ScanParams& p, int c, int& t0, int& n) {
-  if constexpr (VL) {
-    const int2 e = p.chunk_tab[c];
-    t0 = e.x;
-    n = e.y;
-  } else {
-    t0 = c * kC;
-    n = min(kC, p.T - t0);
-  }
-}
 
 
 // l2 normalisation of one row held by TPR consecutive lanes (VI values each),
@@ -636,15 +623,29 @@ __device__ __forceinline__ void lds_wait_all(const unsigned* flags, int n, unsig
   asm volatile("" ::: "memory");
 }
 
+// Token span of chunk c of the work-group's sequence: a sequence's chunks
+// are 64-token steps from its first token (the chunk table holds exactly
+// these spans), so no table is read on the carry's paths; a lookup there
+// makes each step wait for it, and in-order vmcnt then drains every load
+// in flight behind it.
+struct CarryCtx;
+__device__ __forceinline__ void chunk_of(const CarryCtx& x, int c, int& t0, int& n);
+
 struct CarryCtx {
   int h, hk, j0, jc;
   bool col_ok;
   int lane, col, grp;
   int nchunks, cap_chunk, cap_row;
   int c0;             // the sequence's first chunk
+  int t0s, lens;      // the sequence's first token and length
   const float* init;  // the sequence's initial state [Hv][dk][dv] or null
   float* fin;         // its final state or null
 };
+
+__device__ __forceinline__ void chunk_of(const CarryCtx& x, int c, int& t0, int& n) {
+  t0 = x.t0s + c * kC;
+  n = min(kC, x.lens - c * kC);
+}
 
 // EPF elements k.. of raw key row r in a slot's key region, as a CT fragment.
 template <class CT, class IT, int DK>
@@ -714,7 +715,7 @@ template <class CT, class IT, int DK, bool VL>
 __device__ __forceinline__ void carry_keys_slow(const ScanParams& p, const CarryCtx& x, char* keys, int c) {
   typedef Carry<CT, IT, DK> K;
   int t0, n;
-  chunk_at<VL>(p, (VL ? x.c0 : 0) + c, t0, n);
+  chunk_of(x, c, t0, n);
   const char* base = reinterpret_cast<const char*>(static_cast<const IT*>(p.k) + (int64_t)t0 * p.sqk +
                                                    (int64_t)x.hk * p.dk);
   const int64_t rowb = p.sqk * (int64_t)sizeof(IT);
@@ -756,7 +757,7 @@ __device__ __forceinline__ void carry_loader_w(const ScanParams& p, const CarryC
     const int64_t cg = (VL ? x.c0 : 0) + c;
     if constexpr (FAST && KQ1 > KQ0) {
       int t0, n;
-      chunk_at<VL>(p, cg, t0, n);
+      chunk_of(x, c, t0, n);
       const char* base = reinterpret_cast<const char*>(static_cast<const IT*>(p.k) + (int64_t)t0 * p.sqk +
                                                        (int64_t)x.hk * p.dk);
       const int64_t rowb = p.sqk * (int64_t)sizeof(IT);
@@ -869,7 +870,7 @@ __device__ __forceinline__ void carry_recurrence(const ScanParams& p, const Carr
   const uint32_t vrow = (uint32_t)p.sv * (uint32_t)sizeof(IT);
   auto load_v = [&](uint32_t* vb, int c) {
     int t0, n;
-    chunk_at<VL>(p, (VL ? x.c0 : 0) + min(c, x.nchunks - 1), t0, n);
+    chunk_of(x, min(c, x.nchunks - 1), t0, n);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(vbase + (int64_t)t0 * p.sv, n * (int)p.sv * (int)sizeof(IT));
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -1061,7 +1062,7 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
   auto load_o = [&](Ops& o, int c) {
     const int cc = min(c, x.nchunks - 1);
     int t0, n;
-    chunk_at<VL>(p, (VL ? x.c0 : 0) + cc, t0, n);
+    chunk_of(x, cc, t0, n);
     const int64_t cg = (VL ? x.c0 : 0) + cc;
     const frag* nf = static_cast<const frag*>(p.Nf) + (cg * p.Hv + x.h) * G::NBN * 64 + lane;
     const float* scs = p.sc + (cg * p.Hv + x.h) * 256;
@@ -1094,7 +1095,7 @@ __device__ __forceinline__ void carry_outputs(const ScanParams& p, const CarryCt
 #pragma unroll
     for (int b = 0; b < NKT; ++b) yf[b] = hs[(NKX + b) * 64 + lane];
     int t0, n;
-    chunk_at<VL>(p, (VL ? x.c0 : 0) + c, t0, n);
+    chunk_of(x, c, t0, n);
     // rows past the end of the sequence fall outside the buffer range: dropped
     const __amdgpu_buffer_rsrc_t r = make_rsrc(out + (int64_t)t0 * p.so, n * (int)p.so * (int)sizeof(OT));
 #pragma unroll
@@ -1139,13 +1140,21 @@ __global__ __launch_bounds__((Carry<CT, IT, DK>::THREADS)) void scan_carry(ScanP
   x.col = x.lane & 15;
   x.grp = x.lane >> 4;
   const int wave = wave_id();
-  // XCD-aware placement for one sequence: logical work-group L -> consecutive
-  // L share a k-head.  A ragged batch keeps the launch order (sequences with
-  // the most chunks first) across all XCDs instead.
+  // XCD-aware placement: logical work-group L, consecutive L share a k-head,
+  // and work-group b runs on XCD b % 8, so a contiguous eighth of the L of a
+  // sequence goes to each XCD (its k-heads' keys and queries stay in that
+  // XCD's L2).  A ragged batch keeps its launch order (sequences with the most
+  // chunks first) and applies the map within each sequence's block.
   const int nwg = gridDim.x;
-  int L = blockIdx.x;
-  if (!VL && (nwg & 7) == 0) L = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
   const int ntiles = (p.dv + kVT - 1) / kVT;
+  const int per_seq = p.Hv * ntiles;
+  int L = blockIdx.x;
+  if (!VL && (nwg & 7) == 0) {
+    L = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  } else if (VL && (per_seq & 7) == 0) {
+    const int b = L % per_seq;
+    L += (b & 7) * (per_seq >> 3) + (b >> 3) - b;
+  }
   const int rep = p.Hv / p.Hk;
   const int slot = L / (p.Hv * ntiles);
   L -= slot * p.Hv * ntiles;
@@ -1175,6 +1184,13 @@ __global__ __launch_bounds__((Carry<CT, IT, DK>::THREADS)) void scan_carry(ScanP
         x.fin[o] = x.init ? x.init[o] : 0.0f;
       }
     return;
+  }
+  x.t0s = 0;
+  x.lens = p.T;
+  if (VL) {  // the first and last chunk of the sequence
+    const int2 a = p.chunk_tab[x.c0], z = p.chunk_tab[x.c0 + x.nchunks - 1];
+    x.t0s = a.x;
+    x.lens = z.x + z.y - a.x;
   }
   if (wave < K::NREC) {
     if (wave == 0) carry_recurrence<CT, IT, DK, VL, CAP, 0>(p, x, ring, hand, xch, xflag);
