@@ -441,7 +441,7 @@ __device__ __forceinline__ int key_perm16(int r) {
   return (r & ~31) | (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
 }
 
-template <int D>
+template <int D, bool VL>
 __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   constexpr int BQ = 128, BK = 64, NW = 8;
   constexpr int KS = D / 8;           // 16-byte chunks per key row
@@ -461,23 +461,38 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
 
-  // work items dealt as in attn_f16 (longest first, boustrophedon)
-  const int nitems = ((p.qn + BQ - 1) / BQ) * p.heads;
+  // work items dealt as in attn_f16 (longest first, boustrophedon); a ragged
+  // batch's items are its (sequence, query tile) pairs, ranked by key count
+  const int nitems = (VL ? *p.npairs : (p.qn + BQ - 1) / BQ) * p.heads;
   const int nwg = gridDim.x;
   for (int round = 0;; ++round) {
   const int item = round * nwg + ((round & 1) ? nwg - 1 - (int)blockIdx.x : (int)blockIdx.x);
   if (item >= nitems) break;
   const int rank = item / p.heads, hi = item % p.heads;
   const int h = (p.heads & 7) == 0 ? (hi & 7) * (p.heads >> 3) + (hi >> 3) : hi;
-  const int qn = p.qn, kn = p.kn;
-  const int q0 = ((qn + BQ - 1) / BQ - 1 - rank) * BQ;
+  // this item's sequence: queries qb0 + (0..qn-1); keys 0..na-1 from the
+  // prefix buffers, na..kn-1 from rows qb0 + (0..kn-na-1) of k / vt
+  int q0, qb0 = 0, qn = p.qn, kn = p.kn, na = 0;
+  if constexpr (VL) {
+    const int2 e = p.pairs[rank];
+    const int a = min(max(p.cu_q[e.x], 0), p.qn), b = min(max(p.cu_q[e.x + 1], a), p.qn);
+    qb0 = a;
+    qn = b - a;
+    na = p.np;
+    kn = na + qn;
+    q0 = e.y * BQ;
+  } else {
+    q0 = ((qn + BQ - 1) / BQ - 1 - rank) * BQ;
+  }
   const int kvh = h / (p.heads / p.kvh);
   const int offset = kn - qn;
   const int d = p.d;
 
-  const half_t* Q = static_cast<const half_t*>(p.q) + (int64_t)h * p.ldq * d;
-  const half_t* Kb = static_cast<const half_t*>(p.k) + (int64_t)kvh * p.ldk * d;
-  const half_t* Vb = static_cast<const half_t*>(p.vt) + (int64_t)kvh * d * p.ldv;
+  const half_t* Q = static_cast<const half_t*>(p.q) + (int64_t)h * p.ldq * d + (int64_t)qb0 * d;
+  const half_t* Kb = static_cast<const half_t*>(p.k) + (int64_t)kvh * p.ldk * d + (int64_t)qb0 * d;
+  const half_t* Vb = static_cast<const half_t*>(p.vt) + (int64_t)kvh * d * p.ldv + qb0;
+  const half_t* Kp = VL && p.pk ? static_cast<const half_t*>(p.pk) + (int64_t)kvh * p.ldpk * d : nullptr;
+  const half_t* Vp = VL && p.pvt ? static_cast<const half_t*>(p.pvt) + (int64_t)kvh * d * p.ldpv : nullptr;
 
   // Q^T fragments (B operand): lane (n, g) holds d = 32 s + 8 g .. + 7 of its query
   half8 qf[NKS];
@@ -496,7 +511,10 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   // lane % 8 holding keys 8 c .. 8 c + 7 with c = slot ^ ((row >> 1) & 7).
   // d past the head width reads in-bounds data that multiplies zero queries
   // (K) or lands in unstored outputs (V); the last tile clamps keys to kn - 1
-  // (K, masked) and ldv - 8 (V, zeroed below).
+  // (K, masked) and the row end (V, zeroed below).  Ragged batches: tiles
+  // inside the prefix (K) or inside the sequence's own keys take the fast
+  // path from their segment's base; the rest pick each row's segment
+  // (na % 8 == 0 keeps 8-key chunks whole).
   uint32_t ko[NDK], vo[NDV];
   int kr[NDK];
 #pragma unroll
@@ -512,30 +530,38 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
     const int vc = 8 * ((lane & 7) ^ ((vrow >> 1) & 7));
     vo[q] = 2u * (uint32_t)(min(vrow, d - 1) * (int)p.ldv + vc);
   }
-  const int kn1 = kn - 1, ldv8 = (int)p.ldv - 8;
+  const int kn1 = kn - 1, ldv8 = (int)p.ldv - 8 - qb0;
   auto issue_k = [&](int buf, int j0) {
-    if (j0 + BK <= kn) {
+    if (j0 >= na && j0 + BK <= kn) {
+      const half_t* kb = Kb + (int64_t)(j0 - na) * d;
 #pragma unroll
-      for (int q = 0; q < NDK; ++q) dma16s(Kb + (int64_t)j0 * d, ko[q], &sK[buf][(wave * NDK + q) * 512]);
+      for (int q = 0; q < NDK; ++q) dma16s(kb, ko[q], &sK[buf][(wave * NDK + q) * 512]);
+    } else if (j0 + BK <= na) {
+      const half_t* kb = Kp + (int64_t)j0 * d;
+#pragma unroll
+      for (int q = 0; q < NDK; ++q) dma16s(kb, ko[q], &sK[buf][(wave * NDK + q) * 512]);
     } else {
 #pragma unroll
       for (int q = 0; q < NDK; ++q) {
         const int key = min(j0 + kr[q], kn1);
-        const char* src = reinterpret_cast<const char*>(Kb + (int64_t)key * d) + (ko[q] - 2u * (uint32_t)(kr[q] * d));
+        const half_t* row = key < na ? Kp + (int64_t)key * d : Kb + (int64_t)(key - na) * d;
+        const char* src = reinterpret_cast<const char*>(row) + (ko[q] - 2u * (uint32_t)(kr[q] * d));
         dma16(src, &sK[buf][(wave * NDK + q) * 512]);
       }
     }
   };
   auto issue_v = [&](int buf, int j0) {
-    if (j0 + BK <= kn) {
+    if (j0 >= na && j0 + BK <= kn) {
 #pragma unroll
-      for (int q = 0; q < NDV; ++q) dma16s(Vb + j0, vo[q], &sV[buf][(wave * NDV + q) * 512]);
+      for (int q = 0; q < NDV; ++q) dma16s(Vb + (j0 - na), vo[q], &sV[buf][(wave * NDV + q) * 512]);
     } else {
 #pragma unroll
       for (int q = 0; q < NDV; ++q) {
         const int vrow = min((wave * NDV + q) * 8 + (lane >> 3), d - 1);
         const int c0 = j0 + 8 * ((lane & 7) ^ ((((wave * NDV + q) * 8 + (lane >> 3)) >> 1) & 7));
-        dma16(Vb + ((int64_t)vrow * p.ldv + min(c0, ldv8)), &sV[buf][(wave * NDV + q) * 512]);
+        const half_t* src = c0 < na ? Vp + (int64_t)vrow * p.ldpv + c0
+                                    : Vb + ((int64_t)vrow * p.ldv + min(c0 - na, ldv8));
+        dma16(src, &sV[buf][(wave * NDV + q) * 512]);
       }
     }
   };
@@ -700,7 +726,7 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   lt += __shfl_xor(lt, 32, 64);
   const float inv = 1.0f / lt;
   const int row = q0 + 16 * wave + n;
-  const int64_t prow = min(row, qn - 1);
+  const int64_t prow = qb0 + min(row, qn - 1);  // packed row (clamped for the loads)
   const half_t* gate = static_cast<const half_t*>(p.gate) + prow * p.ldg + (int64_t)h * p.hsg;
   half_t* y = static_cast<half_t*>(p.y) + prow * p.ldy + (int64_t)h * d;
   auto out4 = [&](int t, half4 gv) {
@@ -814,19 +840,23 @@ int launch_w8(const AttnParams& p0, hipStream_t s) {
   if (cached[dev] == 0) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16_w8<D>, 512, 0) != hipSuccess || per <= 0) per = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16_w8<D, false>, 512, 0) != hipSuccess || per <= 0) per = 1;
     cached[dev] = cus * per;
   }
-  const int items = (p.qn + 127) / 128 * p.heads;
+  const int qtiles = p.cu_q ? (p.qn + 127) / 128 + p.nseq : (p.qn + 127) / 128;
+  const int items = qtiles * p.heads;
   const int groups = items < cached[dev] ? items : cached[dev];
-  hipLaunchKernelGGL((attn_f16_w8<D>), dim3(groups), dim3(512), 0, s, p);
+  if (p.cu_q)
+    hipLaunchKernelGGL((attn_f16_w8<D, true>), dim3(groups), dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_f16_w8<D, false>), dim3(groups), dim3(512), 0, s, p);
   return check_launch("attention");
 }
 
 }  // namespace
 
-// Workspace: pairs [tiles] int2, keys [tiles] int, the pair count, spans
-// [nseq + 1] int, each region 256-byte aligned.
+// Workspace: pairs [tiles] int2, the pair count, spans [nseq + 1] int, each
+// region 256-byte aligned.
 namespace {
 size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace
@@ -861,7 +891,7 @@ bool attn_f16_ok(const AttnParams& p) {
 }
 
 int attn_f16_launch(const AttnParams& p, hipStream_t s) {
-  if (kW8 && !p.cu_q && p.d > 128) return launch_w8<256>(p, s);
+  if (kW8 && p.d > 128) return launch_w8<256>(p, s);
   if (p.d <= 64) return launch<64>(p, s);
   if (p.d <= 128) return launch<128>(p, s);
   return launch<256>(p, s);
