@@ -216,11 +216,16 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
   const int t0 = blockIdx.y * kConvRun;
   const int t1 = min(t0 + kConvRun, T);
   constexpr int R = kConvRun + 3;
-  Row8<TI> raw[R];  // raw[r]: packed token t0 - 3 + r
+  // raw[r]: packed token t0 - 3 + r, the row index clamped into [0, T) so
+  // every load is unconditional and all stay in flight together (loads under
+  // per-row branches were each awaited before the next); rows outside the
+  // batch are never used (the first run resolves its taps per token, and no
+  // tap reads past the last token)
+  Row8<TI> raw[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int tp = t0 - 3 + r;
-    if (tp >= 0 && tp < T) raw[r].load(x + (int64_t)tp * ldx + c0);
+    const int tp = min(max(t0 - 3 + r, 0), T - 1);
+    raw[r].load(x + (int64_t)tp * ldx + c0);
   }
   float wt[8][4];
   if (taps == 4 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
