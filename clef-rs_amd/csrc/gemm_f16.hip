@@ -483,9 +483,9 @@ int launch(const GemmParams& p, hipStream_t s) {
   // More tiles than CUs: one persistent work-group per CU runs its tiles
   // back to back, requesting the next tile's first stages during the last
   // stages of the current one (no prologue wait, no gap between work-groups).
-  // It stages the epilogue in f16 in the freed slots: 256- and 192-wide
-  // tiles (two activation slots), f16 output, the store and SwiGLU epilogues.
-  if constexpr (NSA == 2 && EPI != 1) {
+  // It stages the epilogue in f16 in the slots the last stage frees: f16
+  // output, the store and SwiGLU epilogues.
+  if constexpr (EPI != 1) {
     if (p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2) {
       hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, true>), dim3(cus), dim3(VM * 128), 0, s, p);
       return check_launch("gemm");

@@ -63,13 +63,14 @@ def test_gemm_projection_shapes(clef, N, dtype):
 
 
 @gpu
-@pytest.mark.parametrize("M,N,K", [(2100, 12300, 128), (2100, 12300, 2048), (2048, 9216, 2048), (4096, 12288, 192)])
+@pytest.mark.parametrize("M,N,K", [(2100, 12300, 128), (2100, 12300, 2048), (2048, 9216, 2048), (4096, 12288, 192),
+                                   (2100, 2100, 256)])  # the last: 289 tiles of 128 x 128
 def test_gemm_persistent_launches(clef, M, N, K):
     """More tiles than CUs: one work-group per CU runs several tiles, the
     next tile's first stages requested during the current one's last.
     Ragged rows and columns, two K stages, a partial last round, 192-wide
-    tiles; the f32 output (one tile per work-group) must agree bit for bit
-    once rounded."""
+    tiles, 128 x 128 tiles (three-slot rings); the f32 output (one tile per
+    work-group) must agree bit for bit once rounded."""
     x, w = _inputs(9, M, N, K, torch.float16)
     y = clef.gemm(x, w)
     _check_f16(y, x, w)
