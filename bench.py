@@ -51,7 +51,40 @@ def parse():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size reference for "
                          "HBM byte counters under rocprofv3 --pmc)")
+    ap.add_argument("--only", choices=("gemm", "attention", "scan"), default=None,
+                    help="run five calls of one kernel workload and exit (for counter profiles): the f16 "
+                         "projection GEMM 4096 x 12288 x 2048, the attention core at T=4096 (16 q / 2 kv "
+                         "heads, d=256), or the full-layer scan (mixed profile)")
     return ap.parse_args()
+
+
+def only_workload(name, torch):
+    """Five calls of one kernel on seeded inputs, nothing else on the GPU:
+    the program a rocprofv3 counter pass of that kernel runs."""
+    import clef_hip
+    import workloads
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    if name == "gemm":
+        x, w = workloads.gemm_inputs(1, 4096, 12288, 2048, dtype=torch.float16, device=dev)
+        y = torch.empty((4096, 12288), dtype=torch.float16, device=dev)
+        fn = lambda: clef_hip.gemm(x, w, out=y)
+    elif name == "attention":
+        T, H, KV, d = 4096, 16, 2, 256
+        q = torch.randn((H, T, d), generator=gen, device=dev).half()
+        k = torch.randn((KV, T, d), generator=gen, device=dev).half()
+        vt = torch.randn((KV, d, T), generator=gen, device=dev).half()
+        gate = torch.randn((T, H, d), generator=gen, device=dev).half()
+        fn = lambda: clef_hip.attention_gated(q, k, vt, gate)
+    else:
+        q, k, v, g, beta = workloads.scan_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16, device=dev)
+        out = torch.empty((4096, 32, 128), device=dev)
+        scan = clef_hip.DeltaScan(128, 128, "mixed")
+        fn = lambda: scan.prefill(q, k, v, g, beta, out=out, want_final=True)
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    print(json.dumps({"only": name, "calls": 5}), flush=True)
 
 
 def measured_traffic(T, profile):
@@ -220,6 +253,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.only:
+        only_workload(args.only, torch)
+        return
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -273,7 +309,10 @@ def main():
         "data": "synthetic (seeded random-init weights N(0,0.02), uniform token ids)",
         "config": {
             "workload": f"hybrid block prefill: 3 gated-DeltaNet + 1 gated GQA attention layer, hidden 2048, "
-                        f"SwiGLU 6144, T={T}, {'mixed-f16' if dt == 'f16' else 'f32'} profile",
+                        f"SwiGLU 6144, T={T}, " + (
+                            "mixed-f16 profile (f16 projection operands, f32 accumulation and residual; the "
+                            "scan on f16 MFMA with f32 accumulation, its f32 state rounded to f16 as the "
+                            "products' operand each chunk)" if dt == "f16" else "f32 profile"),
             "tokens": T, "global_batch": 1, "seq_len": T, "layers": 4,
         },
         "roofline": {
@@ -308,7 +347,16 @@ def main():
     if args.sweep:
         line["gemm_2048"] = gemm_sweep(clef_hip, workloads, torch, dev, args.steps, args.warmup)
         if args.profile == "mixed":
-            del model
+            # the reference's own mixed profile: f16 projections, the whole
+            # recurrence in f32 (qwen.rs:843-848)
+            mref = clef_hip.Backbone(cfg, weights, profile="mixed", scan_precision="strict",
+                                     max_tokens=max(8192, T))
+            msr = event_ms(lambda: mref.prefill(ids, hidden=hidden), args.steps, args.warmup, torch)
+            line["mixed_f16_gemm_f32_scan"] = {
+                "tok_s": round(T / (msr / 1e3), 1), "ms_per_step": round(msr, 4), "steps": args.steps,
+                "profile": "f16 projections with f32 accumulation, scan in f32 on f32 MFMA (the reference's "
+                           "mixed profile: the recurrence stays f32)"}
+            del mref, model
             torch.cuda.empty_cache()
             m32 = clef_hip.Backbone(cfg, weights, profile="f32", max_tokens=max(8192, T))
             ms32 = event_ms(lambda: m32.prefill(ids, hidden=hidden), max(2, args.steps // 3), 1, torch)

@@ -834,18 +834,25 @@ int launch_w8(const AttnParams& p0, hipStream_t s) {
   AttnParams p = p0;
   p.vec_io = ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.y)) & 7) == 0 &&
              p.ldg % 4 == 0 && p.hsg % 4 == 0 && p.ldy % 4 == 0 && p.d % 4 == 0;
-  static int cached[64] = {0};
+  // resident work-groups (CUs x occupancy) of the instance launched, per
+  // device: the ragged instance carries the prefix-segment logic and may fit
+  // fewer per CU, and a grid above the resident count would lose the
+  // longest-first item order
+  static int cached[64][2] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] == 0) {
+  const int vl = p.cu_q ? 1 : 0;
+  if (cached[dev][vl] == 0) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16_w8<D, false>, 512, 0) != hipSuccess || per <= 0) per = 1;
-    cached[dev] = cus * per;
+    const hipError_t e = vl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16_w8<D, true>, 512, 0)
+                            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_f16_w8<D, false>, 512, 0);
+    if (e != hipSuccess || per <= 0) per = 1;
+    cached[dev][vl] = cus * per;
   }
   const int qtiles = p.cu_q ? (p.qn + 127) / 128 + p.nseq : (p.qn + 127) / 128;
   const int items = qtiles * p.heads;
-  const int groups = items < cached[dev] ? items : cached[dev];
+  const int groups = items < cached[dev][vl] ? items : cached[dev][vl];
   if (p.cu_q)
     hipLaunchKernelGGL((attn_f16_w8<D, true>), dim3(groups), dim3(512), 0, s, p);
   else

@@ -197,6 +197,11 @@ __device__ __forceinline__ int seq_of(const int* __restrict__ cu, int nseq, int 
   }
   return lo;
 }
+// First token of t's sequence, clamped into [0, t] (a no-op for a valid
+// table; for any other, rows derived from it stay inside the batch).
+__device__ __forceinline__ int seq_start(const int* __restrict__ cu, int nseq, int t) {
+  return min(max(cu[seq_of(cu, nseq, t)], 0), t);
+}
 
 // Ragged batch of the vectorised conv: tokens cu[s] .. cu[s+1]-1 form sequence
 // s, whose first taps-1 inputs come from its history rows (hist + s * hs, f32
@@ -282,7 +287,10 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
     const int t = t0 + u;
     if (t >= t1) break;
     while (s + 1 < nseq && cu[s + 1] <= t) ++s;
-    const int start = cu[s];
+    // the sequence's first token clamped into [0, t]: a no-op for a valid
+    // table, and for any other every row read below stays inside x or the
+    // history rows
+    const int start = min(max(cu[s], 0), t);
     // a delay reaching before the sequence's history contributes no term (as
     // the single-sequence kernel does before row 0)
     const int avail = hrows + (t - start);
@@ -317,7 +325,7 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_scalar(const void* x, in
   if (idx >= (int64_t)T * W) return;
   const int t = static_cast<int>(idx / W), c = static_cast<int>(idx % W);
   const int s = seq_of(cu, nseq, t);
-  const int start = cu[s];
+  const int start = min(max(cu[s], 0), t);  // seq_start: as in the vectorised kernel
   float acc = 0.0f;
   for (int tap = 0; tap < taps; ++tap) {
     const int tp = t - (taps - 1 - tap);  // packed row of this delay
@@ -526,7 +534,7 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int6
   const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, inv_width), eps));
   const int half = rot / 2;
   // position: pos0 + t, or pos0 + (t - first token of t's sequence)
-  const float p = static_cast<float>(pos0 + (cu ? t - cu[seq_of(cu, nseq, t)] : t));
+  const float p = static_cast<float>(pos0 + (cu ? t - seq_start(cu, nseq, t) : t));
   const int64_t dst = ((int64_t)h * ldy_tok + dst_offset + t) * d;
   for (int i = lane; i < d; i += 64) {
     const float v = rnd(mul_rn(mul_rn(ld(x, src + i, dti), inverse), w[i]), dto);
@@ -560,7 +568,7 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = rot / 2;
   // position: pos0 + t, or pos0 + (t - first token of t's sequence)
-  const float p = static_cast<float>(pos0 + (cu ? t - cu[seq_of(cu, nseq, t)] : t));
+  const float p = static_cast<float>(pos0 + (cu ? t - seq_start(cu, nseq, t) : t));
   for (int f = threadIdx.x; f < half; f += 256) {
     const float ang = mul_rn(p, tab.inv_freq[f]);
     cs[f] = cosf(ang);

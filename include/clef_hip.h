@@ -70,12 +70,15 @@ int clef_delta_scan(const void* q, const void* k, const void* v, int64_t sqk, in
  * allocate device memory (code under HIP graph capture, serving loops or
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
  * scan's scratch is a file-scope device array of CLEF_SCAN_SCRATCH_BYTES
- * (96 MiB) in this library, one per GPU, held until the process ends (its
- * address is looked up once per device, at the first call with that device
- * current; the stream must belong to the current device).  A shape whose
+ * (96 MiB) in this library, one per GPU: the runtime reserves it on each GPU
+ * when it loads the library's device code there, whether or not this entry
+ * point is ever called, and holds it until the process ends (its address is
+ * looked up once per device, at the first call with that device current;
+ * the stream must belong to the current device).  A shape whose
  * clef_delta_scan_workspace exceeds it is rejected before any launch (the
  * full layer shape T = 4096, Hk = 16, Hv = 32, dk = dv = 128 needs 50.5 MiB in
- * the mixed profile and 99 MiB, which is refused, in the strict one).  Arguments and results as clef_delta_scan.  Every call
+ * the mixed profile and 99 MiB, which is refused, in the strict one).
+ * Arguments and results as clef_delta_scan.  Every call
  * on a GPU uses that GPU's one array: calls that overlap in time on one GPU
  * (other streams, other threads) race, and the caller must serialize them.
  */
@@ -102,12 +105,18 @@ int clef_delta_scan_noalloc(const void* q, const void* k, const void* v, int64_t
 size_t clef_delta_scan_varlen_workspace(int T, int nseq, int Hk, int Hv, int dk, int dv, int chunk,
                                         int precision);
 /*
- * Ragged batches and malformed offsets: every entry point that takes
- * cu_seqlens first makes the offsets monotone, R[j] = max over i <= j of
- * cu_seqlens[i] clamped to [0, T], and sequence s is then tokens R[s] ..
- * R[s+1]-1 (R equals cu_seqlens for a valid table).  So an offset table the
- * host cannot inspect (it is device memory) never takes a kernel outside its
- * buffers.  clef_ragged_plan evaluates the same tables on the host, with the
+ * Ragged batches and malformed offsets: the scan (clef_delta_scan_varlen)
+ * and attention (clef_attention_gated_varlen) first make the offsets
+ * monotone, R[j] = max over i <= j of cu_seqlens[i] clamped to [0, T], and
+ * sequence s is then tokens R[s] .. R[s+1]-1 (R equals cu_seqlens for a
+ * valid table).  The conv (clef_conv_silu_varlen) and the q/k norm + rotary
+ * (clef_qk_norm_rotary_varlen) find a token t's sequence by binary search
+ * over cu_seqlens as given and clamp that sequence's first token into
+ * [0, t]; for a valid table this is the same partition.  So an offset table
+ * the host cannot inspect (it is device memory) never takes a kernel outside
+ * its buffers: a malformed one gives unspecified values, never an access
+ * out of bounds.  clef_ragged_plan evaluates the scan's and attention's
+ * tables on the host, with the
  * device kernels' code: cu_seqlens in host memory; unit 64 (the scan's
  * chunks) or 128 (attention's query tiles); spans receives R ([nseq + 1]);
  * table, if not NULL, receives the units (scan: {first token, tokens} per

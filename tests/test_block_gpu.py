@@ -14,7 +14,9 @@ Bars (elementwise, |actual - expected| <= atol + rtol |expected|):
   of the activations' typical size, so elements near zero need a floor; it is
   set by the RMS of the expected values, not their maximum);
 - decisions (the argmax of the 3-logit pooled head, qwen.rs last-token
-  pooling) must equal the oracle's exactly, at 64 positions of the block.
+  pooling) must equal the oracle's exactly: at 64 positions of the block at
+  T = 2048, at 64 positions of the benchmarked T = 4096 prefill, and at 128
+  positions over eight independently seeded 1024-token sequences.
 Achieved errors are appended to the JSON file named by CLEF_PARITY_LOG.
 """
 import ctypes
@@ -243,6 +245,93 @@ def test_block_prefill_matches_oracle(clef, block_case, profile):
             min_margin=float(margins.min()), max_logit_err=float(np.abs(logits - ref_logits).max()))
     assert (np.argmax(logits, 1) == np.argmax(ref_logits, 1)).all(), (
         np.flatnonzero(np.argmax(logits, 1) != np.argmax(ref_logits, 1)), margins.min())
+
+
+BENCH_T = 4096
+BENCH_POSITIONS = np.arange(63, BENCH_T, 64)  # 64 decisions spread over the whole prefill
+
+
+@pytest.fixture(scope="module")
+def bench_case():
+    """The benchmarked workload itself: the block at T = 4096, seed 3 (the
+    token ids bench.py times), with the oracle's hidden states (f32, and with
+    f64-accumulated projection dots) and its logits at 64 positions."""
+    import workloads
+    cfg = workloads.block_config()
+    w = workloads.block_weights(cfg, seed=3)
+    ids = workloads.block_ids(cfg, BENCH_T, seed=3).numpy()
+    head = workloads.block_head(cfg, seed=3)
+    orc, remap = _oracle_backbone(cfg, w, [ids])
+    ref, _ = orc.prefill(remap(ids))
+    with oracle.exact_dots():
+        exact, _ = orc.prefill(remap(ids))
+    ref_logits = ref[BENCH_POSITIONS].astype(np.float64) @ head.cpu().numpy().astype(np.float64).T
+    return cfg, w, ids, head, ref, ref_logits, exact
+
+
+@gpu
+@pytest.mark.parametrize("profile", ["f32", "mixed"])
+def test_block_bench_workload_T4096_matches_oracle(clef, bench_case, profile):
+    """The prefill bench.py times (3 DeltaNet + 1 gated attention layer,
+    hidden 2048, T = 4096, seed 3): hidden states within the profile's bar
+    (f32 against the f64-dot oracle, as at T = 2048) and the pooled head's
+    decision equal to the oracle's at 64 positions over all 4096 tokens."""
+    cfg, w, ids, head, ref, ref_logits, exact = bench_case
+    b = clef.Backbone(cfg, w, profile=profile, max_tokens=8192)
+    hidden, _ = b.prefill(ids)
+    got = hidden.cpu().numpy()
+    if profile == "f32":
+        _record("block T=4096 f32 vs f32 oracle", **_errors(got, ref))
+        _close(got, exact, 1e-5, 1e-4, "block T=4096 f32 vs exact-accumulation oracle")
+    else:
+        _mixed_close(got, ref, "block T=4096 mixed vs oracle")
+    logits = _decisions(clef, hidden, head, BENCH_POSITIONS)
+    margins = _margins(ref_logits)
+    err = np.abs(logits - ref_logits).max()
+    _record(f"block T=4096 {profile} decisions", decisions=len(BENCH_POSITIONS), min_margin=float(margins.min()),
+            max_logit_err=float(err), margin_over_err=float(margins.min() / max(err, 1e-30)))
+    assert (np.argmax(logits, 1) == np.argmax(ref_logits, 1)).all(), (
+        np.flatnonzero(np.argmax(logits, 1) != np.argmax(ref_logits, 1)), margins.min())
+
+
+SEEDED_RUNS = tuple(range(10, 18))  # eight independently seeded token sequences
+SEEDED_T = 1024
+SEEDED_POSITIONS = np.arange(63, SEEDED_T, 64)
+
+
+@pytest.fixture(scope="module")
+def seeded_case(block_case):
+    """Eight token sequences of 1024 ids (seeds 10..17) through the seed-3
+    block weights, with the oracle's logits at 16 positions of each."""
+    import workloads
+    cfg, w, _, head, _, _, _ = block_case
+    runs = [workloads.block_ids(cfg, SEEDED_T, seed=sd).numpy() for sd in SEEDED_RUNS]
+    orc, remap = _oracle_backbone(cfg, w, runs)
+    hv = head.cpu().numpy().astype(np.float64)
+    refs = [orc.prefill(remap(r))[0][SEEDED_POSITIONS].astype(np.float64) @ hv.T for r in runs]
+    return cfg, w, head, runs, refs
+
+
+@gpu
+@pytest.mark.parametrize("profile", ["f32", "mixed"])
+def test_block_decisions_over_seeded_sequences(clef, seeded_case, profile):
+    """128 decisions over eight independently seeded sequences (16 positions
+    each): the device path's argmax equals the oracle's at every one.  The
+    ratio of the smallest margin to the largest logit error is recorded."""
+    cfg, w, head, runs, refs = seeded_case
+    b = clef.Backbone(cfg, w, profile=profile)
+    min_margin, max_err, wrong = np.inf, 0.0, []
+    for i, (ids, ref_logits) in enumerate(zip(runs, refs)):
+        hidden, _ = b.prefill(ids)
+        logits = _decisions(clef, hidden, head, SEEDED_POSITIONS)
+        min_margin = min(min_margin, float(_margins(ref_logits).min()))
+        max_err = max(max_err, float(np.abs(logits - ref_logits).max()))
+        wrong += [(SEEDED_RUNS[i], int(p)) for p in
+                  SEEDED_POSITIONS[np.argmax(logits, 1) != np.argmax(ref_logits, 1)]]
+    _record(f"block seeded sequences {profile} decisions", sequences=len(runs),
+            decisions=len(runs) * len(SEEDED_POSITIONS), min_margin=min_margin, max_logit_err=max_err,
+            margin_over_err=min_margin / max(max_err, 1e-30))
+    assert not wrong, wrong
 
 
 @gpu

@@ -139,6 +139,75 @@ def test_ragged_plan_malformed_tables_stay_in_bounds(clef, unit, cu, T):
     _check_plan(clef, cu, T, unit)
 
 
+def _seq_of(cu, t):
+    """The kernels' binary search: the last s with cu[s] <= t (0 if none)."""
+    lo, hi = 0, len(cu) - 2
+    while lo < hi:
+        mid = (lo + hi + 1) >> 1
+        if cu[mid] <= t:
+            lo = mid
+        else:
+            hi = mid - 1
+    return lo
+
+
+def _conv_varlen_reads(cu, T, hrows, taps, run=16):
+    """Every (buffer, sequence, row) the ragged conv kernels read for a
+    cu_seqlens table, following their index arithmetic (pointwise.hip:
+    conv_silu_varlen_kernel's per-run and per-token paths with rows clamped
+    into [0, T), conv_silu_varlen_scalar, the sequence start clamped into
+    [0, t] by both)."""
+    nseq = len(cu) - 1
+    reads = []
+    if taps <= 4:  # vectorised kernel, runs of `run` tokens
+        for t0 in range(0, T, run):
+            t1 = min(t0 + run, T)
+            reads += [("x", 0, min(max(t0 - 3 + r, 0), T - 1)) for r in range(run + 3)]
+            s = _seq_of(cu, t0)
+            if cu[s] <= t0 - 3 and (s + 1 >= nseq or cu[s + 1] >= t1):
+                continue  # inside one sequence: only the clamped rows above
+            for t in range(t0, t1):
+                while s + 1 < nseq and cu[s + 1] <= t:
+                    s += 1
+                start = min(max(cu[s], 0), t)
+                avail = hrows + (t - start)
+                for k in range(4):
+                    tap, tp = k - (4 - taps), t - 3 + k
+                    if tap >= 0 and avail - (3 - k) >= 0 and tp < start:
+                        reads.append(("hist", s, hrows + tp - start))
+    for t in range(T):  # any-layout kernel
+        s = _seq_of(cu, t)
+        start = min(max(cu[s], 0), t)
+        for tap in range(taps):
+            tp = t - (taps - 1 - tap)
+            hr = hrows + (tp - start)
+            if hr < 0:
+                continue
+            reads.append(("x", 0, tp) if tp >= start and tp >= 0 else ("hist", s, hr))
+    return reads
+
+
+@pytest.mark.parametrize("cu,T", [
+    ([0, 1000, 0, 1000, 0, 1000], 1000),
+    ([0, 5000, 6000], 1000),
+    ([-50, 100, 40, 900, 300, 1000], 1000),
+    ([-7, -3, 2, 1, 40], 40),
+    ([0] * 64 + [64], 64),
+    ([2 ** 31 - 1, -(2 ** 31), 7, 3], 10),
+])
+@pytest.mark.parametrize("hrows,taps", [(0, 4), (3, 4), (1, 2), (7, 8)])
+def test_conv_varlen_malformed_tables_stay_in_bounds(cu, T, hrows, taps):
+    """Any device cu_seqlens table keeps the ragged conv inside x ([T] rows)
+    and the history ([nseq] x [hrows] rows): the sequence start is clamped
+    into [0, t] before any row is derived from it."""
+    if hrows > taps - 1:
+        pytest.skip("history of at most taps - 1 rows")
+    nseq = len(cu) - 1
+    for buf, s, row in _conv_varlen_reads(cu, T, hrows, taps):
+        assert 0 <= s < nseq
+        assert 0 <= row < (T if buf == "x" else hrows), (buf, s, row)
+
+
 def _brute_attention_order(spans):
     """(sequence, tile) pairs in the attention launch order, from its
     definition: key count np + min(128 (t + 1), len) per query tile, most

@@ -173,6 +173,25 @@ def test_swiglu_f32(clef):
 
 
 @gpu
+def test_swiglu_f32_projection_shape(clef):
+    """The f32 SwiGLU the bench times: M = K = 2048, N = 6144 gate and up,
+    x ~ N(0,1), W ~ N(0,0.02) (seeds 1 and 2), against an f64 product; the
+    bound carries each projection's f32 accumulation error (relative to its
+    terms' magnitudes) through silu(g) u."""
+    x, wg = _inputs(1, 2048, 6144, 2048, torch.float32)
+    _, wu = _inputs(2, 2048, 6144, 2048, torch.float32)
+    y = clef.gemm_swiglu(x, wg, wu).double()
+    xd = x.double()
+    g, u = xd @ wg.double().T, xd @ wu.double().T
+    sg, su = xd.abs() @ wg.double().abs().T, xd.abs() @ wu.double().abs().T
+    sil = torch.nn.functional.silu(g)
+    ref = sil * u
+    tol = 1e-5 * (1.1 * sg * u.abs() + sil.abs() * su) + 2e-6 * ref.abs() + 1e-7
+    err = (y - ref).abs()
+    assert (err <= tol).all(), f"max err {err.max().item():.3e}, worst ratio {(err / tol).max().item():.2f}"
+
+
+@gpu
 @pytest.mark.parametrize("dt", [torch.float16, torch.float32])
 def test_silu_mul_matches_the_formula(clef, dt):
     """clef_silu_mul: f32 as silu(g) * u; f16 with the SwiGLU's half roundings,

@@ -222,6 +222,31 @@ def test_conv_silu_varlen_matches_per_sequence_oracle(clef, dt, hist, W):
 
 
 @gpu
+@pytest.mark.parametrize("cu", [[0, 40, 0, 40, 0, 40], [-50, 10, 4, 30, 20, 40], [0, 5000, 6000],
+                                [2 ** 31 - 1, -(2 ** 31), 7, 3]])
+@pytest.mark.parametrize("W", [64, 12])
+def test_conv_and_rotary_varlen_accept_malformed_tables(clef, cu, W):
+    """Device offset tables the host cannot inspect (overlapping, negative,
+    past T, extreme): the ragged conv and q/k rotary kernels clamp each
+    sequence start into [0, t], so they run inside their buffers and give
+    finite values; a valid table is unaffected (tests above)."""
+    T, hist = 40, 3
+    nseq = len(cu) - 1
+    dcu = torch.tensor(cu, dtype=torch.int64).to(torch.int32).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((T, W), generator=gen, device="cuda")
+    w = torch.randn((W, 1, 4), generator=gen, device="cuda") * 0.5
+    h = torch.randn((nseq, hist, W), generator=gen, device="cuda")
+    y = clef.conv_silu_varlen(x, w, dcu, history=h)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    proj = torch.randn((T, 2, 64), generator=gen, device="cuda")
+    r = clef.qk_norm_rotary_varlen(proj, 2, 64, torch.ones(64, device="cuda"), 32, 1e7, dcu)
+    torch.cuda.synchronize()
+    assert torch.isfinite(r).all()
+
+
+@gpu
 def test_qk_norm_rotary_varlen_positions(clef):
     """Ragged batch: token t of sequence s rotates at pos0 + (t - cu[s]),
     i.e. each sequence equals the single-sequence kernel at the same pos0."""

@@ -2,7 +2,7 @@
 per-GPU device array, for callers that cannot allocate) against
 clef_delta_scan with a caller workspace: bit-identical outputs, captured and
 final states on two calls in a row, the second smaller, in both precision
-profiles; shapes whose workspace exceeds the array are rejected before any
+profiles, with the device's free memory unchanged across each call; shapes whose workspace exceeds the array are rejected before any
 launch.  Every call goes through the C ABI."""
 import ctypes as C
 
@@ -24,11 +24,16 @@ def _inputs(seed, T, Hk, Hv, dk, dv, dtype):
     return workloads.scan_inputs(seed, T, Hk, Hv, dk, dv, dtype=dtype)
 
 
-def _call(clef, fn, args, ws=None):
+def _outputs(args):
+    T, Hv, dk, dv, capture, out_dtype = args[7], args[9], args[10], args[11], args[6], args[13]
+    return (torch.empty((T, Hv, dv), dtype=out_dtype, device="cuda"),
+            torch.empty((Hv, dk, dv), device="cuda") if capture else None,
+            torch.empty((Hv, dk, dv), device="cuda"))
+
+
+def _call(clef, fn, args, ws=None, outs=None):
     q, k, v, g, beta, init, capture, T, Hk, Hv, dk, dv, precision, out_dtype = args
-    out = torch.empty((T, Hv, dv), dtype=out_dtype, device="cuda")
-    cap = torch.empty((Hv, dk, dv), device="cuda") if capture else None
-    fin = torch.empty((Hv, dk, dv), device="cuda")
+    out, cap, fin = outs if outs is not None else _outputs(args)
     common = (clef._ptr(q), clef._ptr(k), clef._ptr(v), q.stride(0), v.stride(0), clef._dt(q), clef._ptr(g),
               clef._ptr(beta), g.stride(0), clef._dt(g), T, Hk, Hv, dk, dv, 64, precision, clef._ptr(init),
               capture, clef._ptr(out), Hv * dv, clef._dt(out), clef._ptr(cap), clef._ptr(fin))
@@ -66,6 +71,16 @@ def test_noalloc_scan_equals_workspace_scan(clef, precision):
         got = _call(clef, "clef_delta_scan_noalloc", args)
         torch.cuda.synchronize()
         for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+        # the entry point's defining property: a further call, outputs
+        # allocated beforehand, leaves the device's free memory unchanged
+        outs = _outputs(args)
+        torch.cuda.synchronize()
+        free_before = torch.cuda.mem_get_info()[0]
+        again = _call(clef, "clef_delta_scan_noalloc", args, outs=outs)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free_before
+        for a, b in zip(again, ref):
             assert torch.equal(a, b)
 
 
