@@ -51,24 +51,32 @@ def parse():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size reference for "
                          "HBM byte counters under rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=("gemm", "attention", "scan"), default=None,
+    ap.add_argument("--only", choices=("gemm", "gemm_vendor", "attention", "scan"), default=None,
                     help="run five calls of one kernel workload and exit (for counter profiles): the f16 "
-                         "projection GEMM 4096 x 12288 x 2048, the attention core at T=4096 (16 q / 2 kv "
-                         "heads, d=256), or the full-layer scan (mixed profile)")
+                         "projection GEMM (default 4096 x 12288 x 2048), the same product through "
+                         "torch.matmul (the vendor BLAS, for a side-by-side profile), the attention core at "
+                         "T=4096 (16 q / 2 kv heads, d=256), or the full-layer scan (mixed profile)")
+    ap.add_argument("--gemm-shape", default="4096,12288,2048",
+                    help="M,N,K of --only gemm / gemm_vendor (y[M,N] = x[M,K] . W[N,K]^T, f16 in and out)")
     return ap.parse_args()
 
 
-def only_workload(name, torch):
+def only_workload(name, torch, gemm_shape="4096,12288,2048"):
     """Five calls of one kernel on seeded inputs, nothing else on the GPU:
     the program a rocprofv3 counter pass of that kernel runs."""
     import clef_hip
     import workloads
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(7)
-    if name == "gemm":
-        x, w = workloads.gemm_inputs(1, 4096, 12288, 2048, dtype=torch.float16, device=dev)
-        y = torch.empty((4096, 12288), dtype=torch.float16, device=dev)
-        fn = lambda: clef_hip.gemm(x, w, out=y)
+    if name in ("gemm", "gemm_vendor"):
+        M, N, K = (int(v) for v in gemm_shape.split(","))
+        x, w = workloads.gemm_inputs(1, M, N, K, dtype=torch.float16, device=dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        if name == "gemm":
+            fn = lambda: clef_hip.gemm(x, w, out=y)
+        else:  # the same product on the vendor BLAS (hipBLASLt under torch.matmul)
+            wt = w.t()
+            fn = lambda: torch.matmul(x, wt, out=y)
     elif name == "attention":
         T, H, KV, d = 4096, 16, 2, 256
         q = torch.randn((H, T, d), generator=gen, device=dev).half()
@@ -253,15 +261,15 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    if args.only:
-        only_workload(args.only, torch)
-        return
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only:
+        only_workload(args.only, torch, args.gemm_shape)
+        return
     T = args.tokens
     cfg = workloads.block_config()
     weights = workloads.block_weights(cfg, seed=3, device=dev)
@@ -316,7 +324,7 @@ def main():
             "tokens": T, "global_batch": 1, "seq_len": T, "layers": 4,
         },
         "roofline": {
-            "kernel": "projection GEMMs (gemm_f16_dma / gemm_kernel, all launches of a step)",
+            "kernel": "projection GEMMs (gemm_f16_w4 / gemm_f16_dma / gemm_kernel, all launches of a step)",
             "bound": "mfma",
             "achieved": round(gemm_tfs, 2),
             "peak": MFMA_PEAK_TFS[dt],

@@ -15,6 +15,14 @@
 // c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit 16
 // distinct bank groups.  The DMA lanes pick their source chunk so that the
 // lane-ordered LDS writes produce that layout.
+//
+// 256 x 256 tiles run on gemm_f16_w4 instead: four waves (one per SIMD,
+// 128 x 128 each, 256 accumulator registers) whose products, fragment reads
+// and DMA are interleaved in a fixed order, one MFMA at a time; the same
+// rings, layout and epilogue arithmetic, so the results are bit-identical.
+// At 4096 x 12288 x 2048 the matrix cores are busy 0.66 of the time against
+// 0.54 with eight compiler-scheduled waves (in-projection 186 -> 177 us and
+// SwiGLU 188 -> 182 us over 200 back-to-back calls).
 #include <algorithm>
 #include <utility>
 
@@ -468,6 +476,331 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   }
 }
 
+// ---- 256 x 256 tiles on four waves (one per SIMD, 128 x 128 each, 256
+// accumulator registers), with the stage's products, its fragment reads and
+// the DMA of the stage two ahead interleaved by hand: the compiler's own
+// schedule of the eight-wave kernel leaves the matrix cores idle while both
+// waves of a SIMD wait on LDS.  Same rings (A: 2 stages, B: 3), swizzle,
+// tile order and epilogue arithmetic as gemm_f16_dma, so results are
+// bit-identical to it.
+template <int EPI, bool PERSIST>
+__global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
+  constexpr int BM = 256, BN = 256, VM = 2;
+  constexpr int kWaves = VM * 2;
+  constexpr int WM = BM / VM, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  constexpr int NA = BM * 8 / 64 / kWaves, NB = BN * 8 / 64 / kWaves;  // 8 DMA instructions each
+  static_assert(TM == 4 && TN == 4 && NA == 8 && NB == 8, "the hand schedule below assumes 4 x 4 blocks");
+  typedef half8 frag;
+  constexpr int kStA = BM * kBK, kStB = BN * kBK;
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * kStA + 3 * kStB];
+  auto sA = [&](int st) { return smem + st * kStA; };
+  auto sB = [&](int st) { return smem + 2 * kStA + st * kStB; };
+  static_assert(kWaves * 32 * WN * 4 <= (int)sizeof(smem), "one-tile epilogue staging fits");
+  static_assert(kWaves * 32 * WN * 2 <= kStB * 2, "persistent epilogue staging fits one B slot");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  // tile index with XCD-compact placement, as gemm_f16_dma's
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (EPI == 2 ? (p.N + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN);
+  const int ntiles = tiles_m * tiles_n;
+  auto coords = [&](int t, int& tm0, int& tn0) {
+    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    const int group = 4, gsize = group * tiles_n;
+    const int first_m = (t / gsize) * group, gm = min(group, tiles_m - first_m);
+    tm0 = (first_m + (t % gsize) % gm) * BM;
+    tn0 = ((t % gsize) / gm) * (EPI == 2 ? BN / 2 : BN);
+  };
+  int tile = blockIdx.x, m0 = 0, n0 = 0;
+  coords(tile, m0, n0);
+
+  const half_t* X = static_cast<const half_t*>(p.x);
+  const half_t* W = static_cast<const half_t*>(p.w);
+  const half_t* W2 = static_cast<const half_t*>(p.w2);
+  // DMA instruction q of this wave fills LDS slots [64 j, 64 j + 64), j =
+  // wave * 8 + q, as gemm_f16_dma's issue()
+  int lcol[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
+  const int lrow = lane >> 3;
+  auto dma_a = [&](int slot, int tm0, int ks, int q) {
+    const int j = wave * NA + q;
+    const int row = min(tm0 + 8 * j + lrow, p.M - 1);
+    dma16(X + row * (int)p.ldx + lcol[j & 1] + ks * kBK, sA(slot) + j * 512);
+  };
+  auto dma_b = [&](int slot, int tn0, int ks, int q) {
+    const int j = wave * NB + q;
+    const int row = 8 * j + lrow;
+    const half_t* src;
+    if (EPI == 2) {  // wave column wb holds [gate | up] rows of the same outputs
+      const int wb = row / WN, within = row % WN;
+      const int nr = min(tn0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
+      src = (within >= WN / 2 ? W2 : W) + (int64_t)nr * p.ldw;
+    } else {
+      src = W + (int64_t)min(tn0 + row, p.N - 1) * p.ldw;
+    }
+    dma16(src + lcol[j & 1] + ks * kBK, sB(slot) + j * 512);
+  };
+
+  // fragment q of a k-block: A blocks 0..3, then B blocks 4..7
+  const int frow = lane & 31, fkc = lane >> 5;
+  int foff[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) foff[kb] = 2 * (frow * kBK + (((2 * kb + fkc) ^ ((frow >> 1) & 7)) << 3));
+  frag F[2][TM + TN];
+  auto rd = [&](frag* f, int sa, int sb, int kb, int q) {
+    if (q < TM)
+      f[q] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sA(sa)) + wm * WM * kBK * 2 + foff[kb] +
+                                            q * 32 * kBK * 2);
+    else
+      f[q] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sB(sb)) + wn * WN * kBK * 2 + foff[kb] +
+                                            (q - TM) * 32 * kBK * 2);
+  };
+  float16_t acc[TM][TN];
+
+  const int nk = p.K / kBK;
+  // prologue: stages 0 and 1 requested, stage 0 published, its first k-block
+  // read.  Requests complete in issue order, so waiting until NA + NB remain
+  // in flight waits for stage 0.
+#pragma unroll
+  for (int q = 0; q < NA; ++q) dma_a(0, m0, 0, q);
+#pragma unroll
+  for (int q = 0; q < NB; ++q) dma_b(0, n0, 0, q);
+  if (nk > 1) {
+#pragma unroll
+    for (int q = 0; q < NA; ++q) dma_a(1, m0, 1, q);
+#pragma unroll
+    for (int q = 0; q < NB; ++q) dma_b(1, n0, 1, q);
+    vm_wait<NA + NB>();
+  } else {
+    vm_wait_all();
+  }
+  lds_barrier();
+#pragma unroll
+  for (int q = 0; q < TM + TN; ++q) rd(F[0], 0, 0, 0, q);
+
+  // One stage: 4 k-blocks x 16 products.  During k-blocks 0-2, the first 8
+  // products each carry one fragment read of the next k-block; during
+  // k-blocks 0-1, 8 later products carry the DMA of B two stages ahead (into
+  // the slot stage s-1 freed).  In k-block 3 (its fragments already in
+  // registers) the wave waits for its own requests of stage s+1, the barrier
+  // publishes them and frees stage s's A slot, and products 4-11 each carry
+  // one fragment read of stage s+1 and one DMA of A two stages ahead.
+  // has1 / has2: stages s+1 / s+2 exist (compile-time, so the steady state
+  // has no branches between its instructions); the stage-(s+2) requests go
+  // to tile (tm2, tn2) at k-stage ks2.
+  int ca = 0, cb = 0;
+  auto stage = [&](int tm2, int tn2, int ks2, auto has1_t, auto has2_t) {
+    constexpr bool has1 = decltype(has1_t)::value, has2 = decltype(has2_t)::value;
+    const int na2 = ca, nb2 = cb == 0 ? 2 : cb - 1;      // slots of A(s+2) and B(s+2)
+    const int ca1 = ca ^ 1, cb1 = cb == 2 ? 0 : cb + 1;  // slots of stage s+1
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      frag* cur = F[kb & 1];
+      frag* nxt = F[(kb + 1) & 1];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const int i = m >> 2, j = m & 3;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], cur[TM + j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kb < 3) {
+          if (m < 8) rd(nxt, ca, cb, kb + 1, m);
+          if (kb < 2 && m >= 9 && (m & 1) && has2) dma_b(nb2, tn2, ks2, kb * 4 + ((m - 9) >> 1));
+        } else {
+          if (m == 3 && has1) {
+            // in flight after stage s+1's requests: B(s+2) only
+            if (has2)
+              vm_wait<NB>();
+            else
+              vm_wait_all();
+            lds_barrier();
+          }
+          if (m >= 4 && m < 12 && has1) {
+            rd(nxt, ca1, cb1, 0, m - 4);
+            if (has2) dma_a(na2, tm2, ks2, m - 4);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    ca = ca1;
+    cb = cb1;
+  };
+  typedef std::true_type Y_;
+  typedef std::false_type N_;
+
+  const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
+  const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
+  constexpr int OW = EPI == 2 ? WN / 2 : WN;  // output columns per wave
+  constexpr int CPR = OW / 4, PER = 32 * CPR / 64;
+  const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+  auto zero = [&] {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  };
+
+  if constexpr (PERSIST) {
+    // f16 output, more tiles than CUs (nk >= 2, checked by the launch): one
+    // work-group per CU runs the tiles blockIdx.x, blockIdx.x + gridDim.x,
+    // ...; the last two stages of a tile request the next tile's first two,
+    // and the last tile re-requests its own (in bounds, never read), which
+    // keeps one straight-line stage sequence for every tile
+    for (;;) {
+      const int ntile = tile + gridDim.x;
+      const bool next = ntile < ntiles;
+      int nm0 = m0, nn0 = n0;
+      if (next) coords(ntile, nm0, nn0);
+      zero();
+      for (int s = 0; s + 2 < nk; ++s) stage(m0, n0, s + 2, Y_{}, Y_{});
+      stage(nm0, nn0, 0, Y_{}, Y_{});
+      stage(nm0, nn0, 1, Y_{}, Y_{});
+
+      // epilogue: the B slot of this tile's last stage is free (every wave
+      // passed that stage's barrier, and the next request into it is the
+      // next tile's B(2)); each wave stages its 32 x WN slabs there in f16,
+      // rounded once as the stores would be, and as SwiGLU rounds gate and
+      // up before combining them (neural.metal:35-42).  acc[i][j][e] holds
+      // row (e/4)*8 + (lane/32)*4 + e%4, column lane%32 of block (i, j).
+      const int lastb = cb == 0 ? 2 : cb - 1;
+      half_t* const stg = sB(lastb) + wave * (32 * WN);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = to_f16(acc[i][j][e]);
+        const int rbase = m0 + wm * WM + i * 32;
+        const int cbase = n0 + wn * OW;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
+          half4 h = *reinterpret_cast<const half4*>(stg + row * WN + c4 * 4);
+          if constexpr (EPI == 2) {
+            const half4 u = *reinterpret_cast<const half4*>(stg + row * WN + OW + c4 * 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              // the same function as clef_silu_mul's (neural.rs:484-492)
+              const float sh = static_cast<float>(to_f16(silu_hw(static_cast<float>(h[t]))));
+              h[t] = static_cast<half_t>(sh * static_cast<float>(u[t]));
+            }
+          }
+          const int r = rbase + row, c = cbase + c4 * 4;
+          if (r >= p.M) continue;
+          half_t* dst = static_cast<half_t*>(p.y) + (int64_t)r * p.ldy + c;
+          if (yvec && c + 3 < p.N) {
+            *reinterpret_cast<half4*>(dst) = h;
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (c + t < p.N) dst[t] = h[t];
+          }
+        }
+      }
+      if (!next) break;
+      // every wave's staging reads are done before the next tile's first
+      // stage requests B(2) into this slot
+      lds_barrier();
+      tile = ntile;
+      m0 = nm0;
+      n0 = nn0;
+    }
+    vm_wait_all();  // the re-requested stages land before the work-group ends
+  } else {
+    zero();
+    for (int s = 0; s + 2 < nk; ++s) stage(m0, n0, s + 2, Y_{}, Y_{});
+    if (nk >= 2) stage(0, 0, 0, Y_{}, N_{});
+    stage(0, 0, 0, N_{}, N_{});
+
+    // epilogue of a one-tile work-group: the last barrier follows every
+    // wave's last fragment read, so each wave stages 32 x WN f32 slabs in
+    // its own block of the tile buffers (as gemm_f16_dma's)
+    float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = acc[i][j][e];
+      const int rbase = m0 + wm * WM + i * 32;
+      const int cbase = n0 + wn * OW;
+      float4 v[PER], res[PER];
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
+        if (EPI == 2) {
+          const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+          const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
+          auto sw = [](float gv, float uv) {  // as gemm_f16_dma's (neural.metal:35-42)
+            const float gh = static_cast<float>(to_f16(gv));
+            const float sh = static_cast<float>(to_f16(silu_hw(gh)));
+            return sh * static_cast<float>(to_f16(uv));
+          };
+          v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
+        } else {
+          v[q] = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+        }
+      }
+      if (EPI == 1) {  // residual reads all issued before the first store
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
+          const float* src = static_cast<const float*>(p.y) + (int64_t)r * p.ldy + c;
+          if (yvec && r < p.M && c + 3 < p.N) {
+            res[q] = *reinterpret_cast<const float4*>(src);
+          } else {
+            res[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < p.M) {
+              if (c < p.N) res[q].x = src[0];
+              if (c + 1 < p.N) res[q].y = src[1];
+              if (c + 2 < p.N) res[q].z = src[2];
+              if (c + 3 < p.N) res[q].w = src[3];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = q * 64 + lane, r = rbase + idx / CPR, c = cbase + (idx % CPR) * 4;
+        if (r >= p.M) continue;
+        float4 o = v[q];
+        if (EPI == 1) {
+          auto rdd = [&](float x) { return p.dtype_out == 1 ? static_cast<float>(static_cast<half_t>(x)) : x; };
+          o = make_float4(res[q].x + rdd(o.x), res[q].y + rdd(o.y), res[q].z + rdd(o.z), res[q].w + rdd(o.w));
+        }
+        const int64_t off = (int64_t)r * p.ldy + c;
+        if (esz == 2) {
+          half_t* dst = static_cast<half_t*>(p.y) + off;
+          const half_t h[4] = {static_cast<half_t>(o.x), static_cast<half_t>(o.y), static_cast<half_t>(o.z),
+                               static_cast<half_t>(o.w)};
+          if (yvec && c + 3 < p.N) {
+            *reinterpret_cast<half4*>(dst) = half4{h[0], h[1], h[2], h[3]};
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (c + t < p.N) dst[t] = h[t];
+          }
+        } else {
+          float* dst = static_cast<float*>(p.y) + off;
+          if (yvec && c + 3 < p.N) {
+            *reinterpret_cast<float4*>(dst) = o;
+          } else {
+            const float f[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (c + t < p.N) dst[t] = f[t];
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int EPI>
 int launch(const GemmParams& p, hipStream_t s) {
   // three stages where they fit in LDS (128-wide tiles: 3 x 48 KiB, or
@@ -485,13 +818,25 @@ int launch(const GemmParams& p, hipStream_t s) {
   // stages of the current one (no prologue wait, no gap between work-groups).
   // It stages the epilogue in f16 in the slots the last stage frees: f16
   // output, the store and SwiGLU epilogues.
-  if constexpr (EPI != 1) {
-    if (p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2) {
-      hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, true>), dim3(cus), dim3(VM * 128), 0, s, p);
-      return check_launch("gemm");
+  // (256 x 256 tiles: the four-wave kernel, with the same rule)
+  const bool persistent = EPI != 1 && p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2;
+  if constexpr (BM == 256 && BN == 256) {
+    if constexpr (EPI != 1) {
+      if (persistent) {
+        hipLaunchKernelGGL((gemm_f16_w4<EPI, true>), dim3(cus), dim3(256), 0, s, p);
+        return check_launch("gemm");
+      }
     }
+    hipLaunchKernelGGL((gemm_f16_w4<EPI, false>), dim3(ntiles), dim3(256), 0, s, p);
+  } else {
+    if constexpr (EPI != 1) {
+      if (persistent) {
+        hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, true>), dim3(cus), dim3(VM * 128), 0, s, p);
+        return check_launch("gemm");
+      }
+    }
+    hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, false>), dim3(ntiles), dim3(VM * 128), 0, s, p);
   }
-  hipLaunchKernelGGL((gemm_f16_dma<BM, BN, VM, NSA, NSB, EPI, false>), dim3(ntiles), dim3(VM * 128), 0, s, p);
   return check_launch("gemm");
 }
 
