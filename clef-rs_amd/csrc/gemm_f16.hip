@@ -717,9 +717,11 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
     if (nk >= 2) stage(0, 0, 0, Y_{}, N_{});
     stage(0, 0, 0, N_{}, N_{});
 
-    // epilogue of a one-tile work-group: the last barrier follows every
-    // wave's last fragment read, so each wave stages 32 x WN f32 slabs in
-    // its own block of the tile buffers (as gemm_f16_dma's)
+    // epilogue of a one-tile work-group: each wave stages 32 x WN f32 slabs in
+    // its own 16 KiB of the tile buffers (the A slots), which the last stage
+    // may still be reading for a slower wave: the barrier comes first (no
+    // request is in flight: the last two stages issued none)
+    lds_barrier();
     float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
