@@ -227,13 +227,16 @@ __device__ __forceinline__ float l2norm_row(const float* x, float extra, CT* dst
 // scalars (the normalised keys and queries themselves are not stored: the
 // carry multiplies the raw rows and applies the norms as row factors).
 // ---------------------------------------------------------------------------
+constexpr int kPW = 8;  // waves of a scan_prepare work-group
+
 template <class CT, class IT, int DK>
-__global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
+__global__ __launch_bounds__(64 * kPW, 4) void scan_prepare(ScanParams p) {
   typedef Geo<CT, DK> G;
   constexpr int EPF = G::EPF, KB = G::KB, TPK = G::TPK, NKX = G::NKX, NKT = G::NKT, NST = G::NST;
   constexpr int VI = Vec16<IT>::n;       // input elements per 16-byte vector
   constexpr int TPR = DK / VI;           // threads per row
-  constexpr int RPP = 256 / TPR;         // rows per pass
+  constexpr int NT = 64 * kPW;           // threads
+  constexpr int RPP = NT / TPR;          // rows per pass
   constexpr int NPASS = (2 * kC) / RPP;
   constexpr int LDR = DK + EPF;          // sK / sQ pitch (CT)
   constexpr int LDT = kC + EPF;          // sKT / sM pitch (CT)
@@ -304,18 +307,23 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   lds_barrier();
 
   // ---- 2. K^ transposed, Gram tiles
-  for (int it = tid; it < DK * (kC / EPF); it += 256) {
-    const int e = it / (kC / EPF), tok0 = (it % (kC / EPF)) * EPF;
+  // (consecutive lanes take consecutive columns e: their element reads share
+  // a row and hit distinct banks)
+  for (int it = tid; it < DK * (kC / EPF); it += NT) {
+    const int e = it % DK, tok0 = (it / DK) * EPF;
     frag f;
 #pragma unroll
     for (int j = 0; j < EPF; ++j) f[j] = sK[(tok0 + j) * LDR + e];
     *reinterpret_cast<frag*>(sKT + e * LDT + tok0) = f;
   }
-  // 20 lower 16x16 tiles: K^K^T (jobs 0-9) and Q^K^T (jobs 10-19), 5 per wave
-  float4_t gram[5];
+  // 20 lower 16x16 tiles: K^K^T (jobs 0-9) and Q^K^T (jobs 10-19); wave w
+  // takes the jobs w, w + kPW, ...
+  constexpr int JPW = (20 + kPW - 1) / kPW;
+  float4_t gram[JPW];
 #pragma unroll
-  for (int s = 0; s < 5; ++s) {
-    const int job = wave + 4 * s;
+  for (int s = 0; s < JPW; ++s) {
+    const int job = wave + kPW * s;
+    if (job >= 20) break;
     const bool isqk = job >= 10;
     const int idx = isqk ? job - 10 : job;
     const int tr = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
@@ -330,7 +338,7 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
   lds_barrier();  // sK / sQ are dead from here on
   // zeros that no v-head rewrites: the six 16x16 blocks of sTT below its
   // diagonal blocks (Tm above them) and the six tiles of sM above its diagonal
-  for (int e = tid; e < 6 * 256; e += 256) {
+  for (int e = tid; e < 6 * 256; e += NT) {
     const int blk = e >> 8, ra = (e >> 4) & 15, cb = e & 15;
     const int hi = blk >= 3 ? 3 : blk >= 1 ? 2 : 1;  // (hi, lo): (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
     const int lo = blk - hi * (hi - 1) / 2;
@@ -376,8 +384,9 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     lds_barrier();
     // 3b. A (f32) and M (CT) from the Gram tiles
 #pragma unroll
-    for (int s = 0; s < 5; ++s) {
-      const int job = wave + 4 * s;
+    for (int s = 0; s < JPW; ++s) {
+      const int job = wave + kPW * s;
+      if (job >= 20) break;
       const bool isqk = job >= 10;
       const int idx = isqk ? job - 10 : job;
       const int tr = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
@@ -445,9 +454,11 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     //     on MFMA; token tiles of block b are TPK*b + u.  Tm[r][c] = 0 for
     //     r < c, so token blocks kr < b contribute nothing.
     auto u_blocks = [&](const float* wts, frag* dst) {
-      constexpr int WPB = 4 / NKT;     // waves per token block
-      constexpr int SPW = NST / WPB;   // state tiles per wave
+      constexpr int WPB = kPW / NKT < NST ? kPW / NKT : NST;  // waves per token block
+      constexpr int SPW = NST / WPB;                           // state tiles per wave
+      static_assert(WPB >= 1 && NST % WPB == 0, "whole state tiles per wave");
       const int b = wave / WPB;
+      if (b >= NKT) return;  // (narrow keys: more waves than blocks)
       const int s0 = (wave % WPB) * SPW;
       frag af[TPK][NKT];
 #pragma unroll
@@ -478,16 +489,20 @@ __global__ __launch_bounds__(256) void scan_prepare(ScanParams p) {
     u_blocks(sW, static_cast<frag*>(p.Uf) + cv * G::NBU * 64);
     if (chunk == cap_chunk) u_blocks(sWc, static_cast<frag*>(p.Ucf) + (int64_t)h * G::NBU * 64);
     // 3e. N blocks (t, b): N[16t + m][token block b], as N^T = (Tm B)^T M^T;
-    //     wave t.  Nonzero terms need c' <= k <= r.
+    //     wave w: t = w % 4, token blocks [b0, b0 + BPW).  Nonzero terms need
+    //     c' <= k <= r.
     {
-      const int t = wave;
+      constexpr int BPW = NKT * 4 / kPW;  // token blocks per wave
+      static_assert(BPW >= 1 && NKT * 4 % kPW == 0, "whole token blocks per wave");
+      const int t = wave & 3, b0 = (wave >> 2) * BPW;
       const int kmax = (16 * t + 15) / KB;
       frag bm[NKT];
 #pragma unroll
       for (int kb = 0; kb < NKT; ++kb) bm[kb] = load_frag<CT>(sM + (16 * t + col) * LDT + kb * KB + grp * EPF);
       frag* dst = static_cast<frag*>(p.Nf) + cv * G::NBN * 64;
 #pragma unroll
-      for (int b = 0; b < NKT; ++b) {
+      for (int bb = 0; bb < BPW; ++bb) {
+        const int b = b0 + bb;
         float4_t acc[TPK];
 #pragma unroll
         for (int u = 0; u < TPK; ++u) {
@@ -1222,7 +1237,7 @@ __global__ __launch_bounds__((Carry<CT, IT, DK>::THREADS)) void scan_carry(ScanP
 
 template <class CT, class IT, int DK>
 int launch_dk(const ScanParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((scan_prepare<CT, IT, DK>), dim3(p.nchunks, p.Hk), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((scan_prepare<CT, IT, DK>), dim3(p.nchunks, p.Hk), dim3(64 * kPW), 0, stream, p);
   int rc = check_launch("scan_prepare");
   if (rc) return rc;
   const int ntiles = (p.dv + kVT - 1) / kVT;
