@@ -229,8 +229,10 @@ __device__ __forceinline__ float l2norm_row(const float* x, float extra, CT* dst
 // ---------------------------------------------------------------------------
 constexpr int kPW = 8;  // waves of a scan_prepare work-group
 
+// Two work-groups per CU (16 waves, 128 registers each) where the LDS holds
+// two; f32 products with 128-wide keys need more LDS than half a CU.
 template <class CT, class IT, int DK>
-__global__ __launch_bounds__(64 * kPW, 4) void scan_prepare(ScanParams p) {
+__global__ __launch_bounds__(64 * kPW, (sizeof(CT) == 4 && DK > 64) ? 2 : 4) void scan_prepare(ScanParams p) {
   typedef Geo<CT, DK> G;
   constexpr int EPF = G::EPF, KB = G::KB, TPK = G::TPK, NKX = G::NKX, NKT = G::NKT, NST = G::NST;
   constexpr int VI = Vec16<IT>::n;       // input elements per 16-byte vector
