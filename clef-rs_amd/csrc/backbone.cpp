@@ -497,7 +497,14 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
   auto gemm_bytes = [&](double M, double N, double K, bool residual) {
     return da * (M * K + N * K) + (residual ? 8.0 * M * N : da * M * N);
   };
-  TIMED(CLEF_CAT_OTHER, 0, (4.0 + da) * T * H, clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
+  // the embedding and the first layer's input norm in one pass where it applies
+  const bool normed0 =
+      c.n_layers > 0 && embed_rms_applies(b->embeddings, H, h, b->layers[0].in_norm, w.n, H);
+  if (normed0)
+    TIMED(CLEF_CAT_OTHER, 4.0 * T * H, (4.0 + 2.0 * da) * T * H,
+          embed_rms_launch(w.ids, T, b->embeddings, ad, c.vocab, H, h, b->layers[0].in_norm, w.n, H, ad, c.eps, s));
+  else
+    TIMED(CLEF_CAT_OTHER, 0, (4.0 + da) * T * H, clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
   const int Hv = c.lin_v_heads, dv = c.lin_dv, taps = c.conv_taps;
   const int heads = c.heads, kvh = c.kv_heads, d = c.head_dim;
   const int Ttot = offset + T;
@@ -506,7 +513,8 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
   for (int li = 0; li < c.n_layers; ++li) {
     const LayerState& L = b->layers[li];
     CLEF_TRY(control_check(b));  // qwen.rs:380
-    TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
+    if (li > 0 || !normed0)
+      TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
       char* proj = static_cast<char*>(w.proj);
@@ -654,7 +662,14 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
   auto gemm_bytes = [&](double M, double N, double K, bool residual) {
     return da * (M * K + N * K) + (residual ? 8.0 * M * N : da * M * N);
   };
-  TIMED(CLEF_CAT_OTHER, 0, (4.0 + da) * T * H, clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
+  // the embedding and the first layer's input norm in one pass where it applies
+  const bool normed0 =
+      c.n_layers > 0 && embed_rms_applies(b->embeddings, H, h, b->layers[0].in_norm, w.n, H);
+  if (normed0)
+    TIMED(CLEF_CAT_OTHER, 4.0 * T * H, (4.0 + 2.0 * da) * T * H,
+          embed_rms_launch(w.ids, T, b->embeddings, ad, c.vocab, H, h, b->layers[0].in_norm, w.n, H, ad, c.eps, s));
+  else
+    TIMED(CLEF_CAT_OTHER, 0, (4.0 + da) * T * H, clef_embed(w.ids, T, b->embeddings, ad, c.vocab, H, h, s));
   const int Hv = c.lin_v_heads, dv = c.lin_dv, taps = c.conv_taps;
   const int heads = c.heads, kvh = c.kv_heads, d = c.head_dim;
   const double rms_bytes = (4.0 + da) * T * H;
@@ -668,7 +683,8 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
   for (int li = 0; li < c.n_layers; ++li) {
     const LayerState& L = b->layers[li];
     CLEF_TRY(control_check(b));  // qwen.rs:380
-    TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
+    if (li > 0 || !normed0)
+      TIMED(CLEF_CAT_NORM, 4.0 * T * H, rms_bytes, clef_rms_norm(h, H, CLEF_F32, L.in_norm, w.n, H, ad, T, H, c.eps, s));
     if (L.kind == 0) {
       const int NP = b->NP, Wc = b->W;
       char* proj = static_cast<char*>(w.proj);

@@ -159,6 +159,15 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);  // records msg, returns code
 int check_launch(const char* what);          // hipGetLastError -> 0 or >0
 
+// Token embedding fused with the first layer's input RMSNorm (pointwise.hip):
+// writes the f32 residual rows h [T, H] and the normalised rows y (ldy apart).
+// embed_rms_applies: whether the shape and alignment are on its path (H 1024
+// or 2048, 16-byte aligned rows); elsewhere callers run clef_embed and
+// clef_rms_norm.
+bool embed_rms_applies(const void* table, int H, const float* h, const float* w, const void* y, int64_t ldy);
+int embed_rms_launch(const int32_t* ids, int T, const void* table, int dtype_table, int vocab, int H, float* h,
+                     const float* w, void* y, int64_t ldy, int dtype_out, float eps, hipStream_t st);
+
 }  // namespace clef
 
 #define CLEF_REQUIRE(cond, msg)                              \

@@ -344,29 +344,16 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_scalar(const void* x, in
 }
 
 // Row RMSNorm with the row held in registers: one wave per row, VPL values
-// per lane loaded as 4-wide vectors (width == 4 * 64 * (VPL/4) exactly).
+// per lane at columns (i * 64 + lane) * 4 + j (width == 4 * 64 * (VPL/4)
+// exactly).  rms_row_out reduces and writes a row that a kernel has loaded.
 template <int VPL, class TO>
-__global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restrict__ x, int64_t ldx,
-                                                           const float* __restrict__ w, TO* __restrict__ y,
-                                                           int64_t ldy, int rows, int width, float eps,
-                                                           float inv_width) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  float v[VPL];
-  const float* src = x + (int64_t)row * ldx;
-#pragma unroll
-  for (int i = 0; i < VPL / 4; ++i) {
-    const float4_t a = *reinterpret_cast<const float4_t*>(src + (i * 64 + lane) * 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[i * 4 + j] = a[j];
-  }
+__device__ __forceinline__ void rms_row_out(const float* v, int lane, const float* __restrict__ w, TO* dst,
+                                            float eps, float inv_width) {
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) s += v[i] * v[i];
   s = wave_sum(s);
   const float inverse = 1.0f / sqrtf(add_rn(mul_rn(s, inv_width), eps));
-  TO* dst = y + (int64_t)row * ldy;
 #pragma unroll
   for (int i = 0; i < VPL / 4; ++i) {
     const int c = (i * 64 + lane) * 4;
@@ -383,6 +370,60 @@ __global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restri
       *reinterpret_cast<float4_t*>(dst + c) = o;
     }
   }
+}
+
+template <int VPL, class TO>
+__global__ __launch_bounds__(256) void rms_f32_rows_kernel(const float* __restrict__ x, int64_t ldx,
+                                                           const float* __restrict__ w, TO* __restrict__ y,
+                                                           int64_t ldy, int rows, int width, float eps,
+                                                           float inv_width) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float v[VPL];
+  const float* src = x + (int64_t)row * ldx;
+#pragma unroll
+  for (int i = 0; i < VPL / 4; ++i) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(src + (i * 64 + lane) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i * 4 + j] = a[j];
+  }
+  rms_row_out<VPL, TO>(v, lane, w, y + (int64_t)row * ldy, eps, inv_width);
+}
+
+// Token embedding and the first layer's input norm in one pass (the rows of
+// embed_vec_kernel, then rms_f32_rows_kernel's arithmetic on the same
+// values): one wave per token writes its f32 residual row and its normalised
+// row, so the residual is not read back.
+template <int VPL, class TT, class TO>
+__global__ __launch_bounds__(256) void embed_rms_kernel(const int32_t* __restrict__ ids, int T,
+                                                        const TT* __restrict__ table, int vocab,
+                                                        float* __restrict__ h, const float* __restrict__ w,
+                                                        TO* __restrict__ y, int64_t ldy, float eps, float inv_width) {
+  constexpr int H = VPL * 64;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const int id = min(max(ids[row], 0), vocab - 1);
+  const TT* src = table + (int64_t)id * H;
+  float* hrow = h + (int64_t)row * H;
+  float v[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL / 4; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    float4_t a;
+    if constexpr (sizeof(TT) == 2) {
+      const half4 q = *reinterpret_cast<const half4*>(src + c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = static_cast<float>(q[j]);
+    } else {
+      a = *reinterpret_cast<const float4_t*>(src + c);
+    }
+    *reinterpret_cast<float4_t*>(hrow + c) = a;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i * 4 + j] = a[j];
+  }
+  rms_row_out<VPL, TO>(v, lane, w, y + (int64_t)row * ldy, eps, inv_width);
 }
 
 // Gated output norm for rows of 128: 16 lanes per row, 8 values per lane,
@@ -1065,6 +1106,46 @@ extern "C" int clef_embed(const int32_t* ids, int T, const void* table, int dtyp
                      vocab, H, h);
   return check_launch("embed");
 }
+
+namespace clef {
+bool embed_rms_applies(const void* table, int H, const float* h, const float* w, const void* y, int64_t ldy) {
+  return (H == 2048 || H == 1024) && ldy >= H && ldy % 4 == 0 &&
+         ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(w) |
+           reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+}
+
+// Embedding + first input norm (embed_rms_kernel), for the shapes
+// embed_rms_applies accepts.
+int embed_rms_launch(const int32_t* ids, int T, const void* table, int dtype_table, int vocab, int H, float* h,
+                     const float* w, void* y, int64_t ldy, int dtype_out, float eps, hipStream_t st) {
+  CLEF_REQUIRE(ids && table && h && w && y && T >= 1 && vocab >= 1, "embed+norm: arguments");
+  CLEF_REQUIRE(embed_rms_applies(table, H, h, w, y, ldy), "embed+norm: shape or alignment");
+  CLEF_REQUIRE(dtype_ok(dtype_table) && dtype_ok(dtype_out), "embed+norm: dtype");
+  const float inv_w = static_cast<float>(1.0 / static_cast<double>(H));
+  const dim3 g((T + 3) / 4);
+#define CLEF_EMBED_RMS(VPL, TT, TO)                                                                       \
+  hipLaunchKernelGGL((embed_rms_kernel<VPL, TT, TO>), g, dim3(256), 0, st, ids, T, static_cast<const TT*>(table), \
+                     vocab, h, w, static_cast<TO*>(y), ldy, eps, inv_w)
+#define CLEF_EMBED_RMS_T(VPL)                                              \
+  if (dtype_table == CLEF_F16 && dtype_out == CLEF_F16) {                  \
+    CLEF_EMBED_RMS(VPL, half_t, half_t);                                   \
+  } else if (dtype_table == CLEF_F16) {                                    \
+    CLEF_EMBED_RMS(VPL, half_t, float);                                    \
+  } else if (dtype_out == CLEF_F16) {                                      \
+    CLEF_EMBED_RMS(VPL, float, half_t);                                    \
+  } else {                                                                 \
+    CLEF_EMBED_RMS(VPL, float, float);                                     \
+  }
+  if (H == 2048) {
+    CLEF_EMBED_RMS_T(32)
+  } else {
+    CLEF_EMBED_RMS_T(16)
+  }
+#undef CLEF_EMBED_RMS_T
+#undef CLEF_EMBED_RMS
+  return check_launch("embed_rms");
+}
+}  // namespace clef
 
 extern "C" int clef_head_logits(const float* x, int H, const float* w, int n_logits, float* logits,
                                 void* stream) {
