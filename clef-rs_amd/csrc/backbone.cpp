@@ -568,6 +568,9 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
       TIMED(CLEF_CAT_GEMM, 2.0 * T * NA * H, gemm_bytes(T, NA, H, false),
             clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
       const size_t koff = a * 2 * heads * d, voff = koff + a * kvh * d;
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
+            clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim, c.rope_theta,
+                                offset, 0, c.eps, s));
       if (initial) {  // cached keys and values precede the new ones (qwen.rs:486-496)
         for (int g = 0; g < kvh; ++g)
           CLEF_TRY(copy_rows(static_cast<char*>(w.kh) + a * (size_t)g * Ttot * d,
@@ -576,18 +579,9 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
                                  hipMemcpyDeviceToDevice, s),
                 "value prefix copy");
       }
-      if (qk_rotary_pair_applies(d, c.rotary_dim)) {  // query and key heads in one launch
-        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * (heads + kvh) * d,
-              qk_rotary_pair_launch(proj, proj + koff, NA, 2 * d, d, ad, L.q_norm, L.k_norm, w.qh, w.kh, Ttot, offset,
-                                    ad, T, heads, kvh, d, c.rotary_dim, c.rope_theta, offset, c.eps, nullptr, 0, s));
-      } else {
-        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
-              clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
-                                  c.rope_theta, offset, 0, c.eps, s));
-        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
-              clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
-                                  c.rope_theta, offset, offset, c.eps, s));
-      }
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
+            clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
+                                c.rope_theta, offset, offset, c.eps, s));
       TIMED(CLEF_CAT_OTHER, 0, 2.0 * da * T * kvh * d,
             clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, offset, s));
       if (capture) {
@@ -730,18 +724,12 @@ extern "C" int clef_backbone_prefill_varlen(clef_backbone* b, const int32_t* ids
       TIMED(CLEF_CAT_GEMM, 2.0 * T * NA * H, gemm_bytes(T, NA, H, false),
             clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
       const size_t koff = a * 2 * heads * d, voff = koff + a * kvh * d;
-      if (qk_rotary_pair_applies(d, c.rotary_dim)) {  // query and key heads in one launch
-        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * (heads + kvh) * d,
-              qk_rotary_pair_launch(proj, proj + koff, NA, 2 * d, d, ad, L.q_norm, L.k_norm, w.qh, w.kh, T, 0, ad, T,
-                                    heads, kvh, d, c.rotary_dim, c.rope_theta, offset, c.eps, w.cu, nseq, s));
-      } else {
-        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
-              clef_qk_norm_rotary_varlen(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
-                                         c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
-        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
-              clef_qk_norm_rotary_varlen(proj + koff, NA, d, ad, L.k_norm, w.kh, T, ad, T, kvh, d, c.rotary_dim,
-                                         c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
-      }
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
+            clef_qk_norm_rotary_varlen(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
+                                       c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
+      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
+            clef_qk_norm_rotary_varlen(proj + koff, NA, d, ad, L.k_norm, w.kh, T, ad, T, kvh, d, c.rotary_dim,
+                                       c.rope_theta, offset, w.cu, nseq, 0, c.eps, s));
       TIMED(CLEF_CAT_OTHER, 0, 2.0 * da * T * kvh * d,
             clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, 0, s));
       if (!varlen_per_sequence_attention(b, offset)) {

@@ -167,13 +167,6 @@ int check_launch(const char* what);          // hipGetLastError -> 0 or >0
 bool embed_rms_applies(const void* table, int H, const float* h, const float* w, const void* y, int64_t ldy);
 int embed_rms_launch(const int32_t* ids, int T, const void* table, int dtype_table, int vocab, int H, float* h,
                      const float* w, void* y, int64_t ldy, int dtype_out, float eps, hipStream_t st);
-// Query and key norms + rotary of one attention layer in one launch
-// (pointwise.hip), for the head widths qk_rotary_pair_applies accepts.
-bool qk_rotary_pair_applies(int d, int rot_dim);
-int qk_rotary_pair_launch(const void* x_q, const void* x_k, int64_t ldx, int64_t hs_q, int64_t hs_k, int dtype_in,
-                          const float* w_q, const float* w_k, void* y_q, void* y_k, int64_t ldk_tok, int k_offset,
-                          int dtype_out, int T, int heads_q, int heads_k, int d, int rot_dim, double theta, int pos0,
-                          float eps, const int32_t* cu, int nseq, hipStream_t st);
 
 }  // namespace clef
 

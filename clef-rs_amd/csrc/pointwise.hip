@@ -554,19 +554,6 @@ struct RotaryTable {
   float inv_freq[128];
 };
 
-// One set of heads for qk_norm_rotary_tok: rows x (ldx apart, heads hs
-// apart), norm weights w, output y [heads][ldy_tok][D] from row dst_offset;
-// vec: 4-element vector loads and stores allowed.
-template <class TI, class TO>
-struct QkHeads {
-  const TI* x;
-  int64_t ldx, hs;
-  const float* w;
-  TO* y;
-  int64_t ldy_tok;
-  int heads, dst_offset, vec;
-};
-
 __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int64_t ldx, int64_t hs,
                                                              int dti, const float* w, void* y,
                                                              int64_t ldy_tok, int dto, int T,
@@ -612,9 +599,11 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int6
 // Same per-element roundings as qk_norm_rotary_kernel; the squares are
 // summed per lane over consecutive features, then across the wave.
 template <int EPL, class TI, class TO>
-__global__ __launch_bounds__(256) void qk_norm_rotary_tok(QkHeads<TI, TO> A, QkHeads<TI, TO> B, int rot, int pos0,
-                                                          float eps, float inv_width, RotaryTable tab,
-                                                          const int* __restrict__ cu, int nseq) {
+__global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__ x, int64_t ldx, int64_t hs,
+                                                          const float* __restrict__ w, TO* __restrict__ y,
+                                                          int64_t ldy_tok, int heads, int rot, int pos0,
+                                                          int dst_offset, float eps, float inv_width, int vec,
+                                                          RotaryTable tab, const int* __restrict__ cu, int nseq) {
   constexpr int D = 64 * EPL;
   __shared__ float cs[128], sn[128];
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -629,24 +618,17 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(QkHeads<TI, TO> A, QkH
   __syncthreads();
   const int i0 = lane * EPL;
   const int pd = half / EPL;  // partner lane distance
-  float cw[EPL], sw[EPL];
+  float wv[EPL], cw[EPL], sw[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int i = i0 + e;
+    wv[e] = w[i];
     const int f = i < half ? i : i - half;
     cw[e] = i < rot ? cs[f] : 1.0f;
     sw[e] = i < rot ? (i < half ? -sn[f] : sn[f]) : 0.0f;  // r = -v[i + half] below half, v[i - half] above
   }
-  // the heads of set A, then those of set B (the keys beside the queries)
-  for (int hh = wave; hh < A.heads + B.heads; hh += 4) {
-    const bool inb = hh >= A.heads;
-    const QkHeads<TI, TO>& S = inb ? B : A;
-    const int h = inb ? hh - A.heads : hh;
-    float wv[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) wv[e] = S.w[i0 + e];
-    const int vec = S.vec;
-    const TI* src = S.x + (int64_t)t * S.ldx + (int64_t)h * S.hs + i0;
+  for (int h = wave; h < heads; h += 4) {
+    const TI* src = x + (int64_t)t * ldx + (int64_t)h * hs + i0;
     float v[EPL];
     bool got = false;
     if constexpr (EPL == 4) {
@@ -681,7 +663,7 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(QkHeads<TI, TO> A, QkH
       const float vj = __shfl(v[e], plane, 64);
       out[e] = cvt_out<TO>(i0 + e < rot ? add_rn(mul_rn(v[e], cw[e]), mul_rn(vj, sw[e])) : v[e]);
     }
-    TO* dst = S.y + ((int64_t)h * S.ldy_tok + S.dst_offset + t) * D + i0;
+    TO* dst = y + ((int64_t)h * ldy_tok + dst_offset + t) * D + i0;
     bool done = false;
     if constexpr (EPL == 4) {
       if (vec) {
@@ -995,42 +977,21 @@ extern "C" int clef_gated_rms_silu(const void* o, int dtype_o, const void* z, in
 
 // per-token kernel when d is 64, 128 or 256 and the rotary half splits into
 // whole lanes; false if not taken (nothing launched)
-// One per-token set of heads for the launcher below (y with ldy_tok tokens
-// per head, written from row dst_offset).
-struct QkSet {
-  const void* x;
-  int64_t ldx, hs;
-  const float* w;
-  void* y;
-  int64_t ldy_tok;
-  int heads, dst_offset;
-};
-
-// qk_norm_rotary_tok for the heads of a and, if b.heads > 0, of b in the same
-// launch (both read with dtype dti, written with dto; same width, rotary and
-// positions).  False when the width is outside the kernel's forms.
-static bool qk_norm_rotary_tok_launch(const QkSet& a, const QkSet& b, int dti, int dto, int T, int d, int rot,
-                                      int pos0, float eps, const RotaryTable& tab, const int* cu, int nseq,
+static bool qk_norm_rotary_tok_launch(const void* x, int64_t ldx, int64_t hs, int dti, const float* w, void* y,
+                                      int64_t ldy_tok, int dto, int T, int heads, int d, int rot, int pos0,
+                                      int dst_offset, float eps, const RotaryTable& tab, const int* cu, int nseq,
                                       hipStream_t st) {
   const int epl = d / 64;
   if (d % 64 != 0 || !(epl == 1 || epl == 2 || epl == 4) || (rot / 2) % epl != 0) return false;
   const int es_in = dti == CLEF_F16 ? 2 : 4, es_out = dto == CLEF_F16 ? 2 : 4;
-  auto vec_ok = [&](const QkSet& q) {
-    return (reinterpret_cast<uintptr_t>(q.x) % (es_in * epl) == 0 && (q.ldx * es_in) % (es_in * epl) == 0 &&
-            (q.hs * es_in) % (es_in * epl) == 0 && reinterpret_cast<uintptr_t>(q.y) % (es_out * epl) == 0)
-               ? 1
-               : 0;
-  };
+  const int vec = (reinterpret_cast<uintptr_t>(x) % (es_in * epl) == 0 && (ldx * es_in) % (es_in * epl) == 0 &&
+                   (hs * es_in) % (es_in * epl) == 0 && reinterpret_cast<uintptr_t>(y) % (es_out * epl) == 0)
+                      ? 1
+                      : 0;
   const float inv = static_cast<float>(1.0 / static_cast<double>(d));
-  auto heads_of = [&](const QkSet& q, auto ti, auto to) {
-    typedef decltype(ti) TI;
-    typedef decltype(to) TO;
-    return QkHeads<TI, TO>{static_cast<const TI*>(q.x), q.ldx, q.hs, q.w, static_cast<TO*>(q.y),
-                           q.ldy_tok, q.heads, q.dst_offset, q.heads > 0 ? vec_ok(q) : 0};
-  };
-#define CLEF_QKR(E, TI, TO)                                                                                   \
-  hipLaunchKernelGGL((qk_norm_rotary_tok<E, TI, TO>), dim3(T), dim3(256), 0, st, heads_of(a, TI(), TO()),      \
-                     heads_of(b, TI(), TO()), rot, pos0, eps, inv, tab, cu, nseq)
+#define CLEF_QKR(E, TI, TO)                                                                                     \
+  hipLaunchKernelGGL((qk_norm_rotary_tok<E, TI, TO>), dim3(T), dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
+                     hs, w, static_cast<TO*>(y), ldy_tok, heads, rot, pos0, dst_offset, eps, inv, vec, tab, cu, nseq)
 #define CLEF_QKR_E(TI, TO)      \
   if (epl == 4)                 \
     CLEF_QKR(4, TI, TO);        \
@@ -1068,8 +1029,8 @@ extern "C" int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int d
   RotaryTable tab{};
   for (int i = 0; i < rot_dim / 2; ++i)  // ops.rs:165: theta.powf(-(2i)/dim) in f64, then f32
     tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
-  if (qk_norm_rotary_tok_launch(QkSet{x, ldx, hs, w, y, ldy_tok, heads, dst_offset}, QkSet{}, dtype_in, dtype_out,
-                                T, d, rot_dim, pos0, eps, tab, nullptr, 0, static_cast<hipStream_t>(stream)))
+  if (qk_norm_rotary_tok_launch(x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d, rot_dim, pos0,
+                                dst_offset, eps, tab, nullptr, 0, static_cast<hipStream_t>(stream)))
     return check_launch("qk_norm_rotary");
   hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
@@ -1077,40 +1038,6 @@ extern "C" int clef_qk_norm_rotary(const void* x, int64_t ldx, int64_t hs, int d
                      tab, nullptr, 0);
   return check_launch("qk_norm_rotary");
 }
-
-namespace clef {
-// Query and key norms + rotary of one attention layer in one launch (the
-// per-token kernel, one rotation table per token): the query heads (x_q,
-// heads_q apart by hs_q) into y_q [heads_q][T][d], then the key heads into
-// y_k [heads_k][ldk_tok][d] from row k_offset.  Both read ldx apart.  cu /
-// nseq: a ragged batch (positions from each sequence's first token), else
-// null / 0.  For the widths qk_rotary_pair_applies accepts (elsewhere callers
-// run clef_qk_norm_rotary twice).
-bool qk_rotary_pair_applies(int d, int rot_dim) {
-  const int epl = d / 64;
-  return d % 64 == 0 && (epl == 1 || epl == 2 || epl == 4) && rot_dim >= 0 && (rot_dim / 2) % epl == 0;
-}
-
-int qk_rotary_pair_launch(const void* x_q, const void* x_k, int64_t ldx, int64_t hs_q, int64_t hs_k, int dtype_in,
-                          const float* w_q, const float* w_k, void* y_q, void* y_k, int64_t ldk_tok, int k_offset,
-                          int dtype_out, int T, int heads_q, int heads_k, int d, int rot_dim, double theta, int pos0,
-                          float eps, const int32_t* cu, int nseq, hipStream_t st) {
-  CLEF_REQUIRE(x_q && x_k && w_q && w_k && y_q && y_k && (!cu || nseq >= 1), "q/k norm pair: null pointer");
-  CLEF_REQUIRE(T >= 1 && heads_q >= 1 && heads_k >= 1 && d >= 1 && hs_q >= d && hs_k >= d,
-               "q/k norm pair: dimensions");
-  CLEF_REQUIRE(rot_dim >= 0 && rot_dim <= d && rot_dim % 2 == 0 && rot_dim / 2 <= 128, "q/k norm pair: rotary width");
-  CLEF_REQUIRE(k_offset >= 0 && ldk_tok >= (int64_t)k_offset + T && pos0 >= 0, "q/k norm pair: destination");
-  CLEF_REQUIRE(dtype_ok(dtype_in) && dtype_ok(dtype_out), "q/k norm pair: dtype");
-  RotaryTable tab{};
-  for (int i = 0; i < rot_dim / 2; ++i)  // as clef_qk_norm_rotary
-    tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
-  CLEF_REQUIRE(qk_rotary_pair_applies(d, rot_dim), "q/k norm pair: head width outside the per-token kernel");
-  qk_norm_rotary_tok_launch(QkSet{x_q, ldx, hs_q, w_q, y_q, T, heads_q, 0},
-                            QkSet{x_k, ldx, hs_k, w_k, y_k, ldk_tok, heads_k, k_offset}, dtype_in, dtype_out, T, d,
-                            rot_dim, pos0, eps, tab, cu, cu ? nseq : 0, st);
-  return check_launch("qk_norm_rotary pair");
-}
-}  // namespace clef
 
 extern "C" int clef_qk_norm_rotary_varlen(const void* x, int64_t ldx, int64_t hs, int dtype_in, const float* w,
                                           void* y, int64_t ldy_tok, int dtype_out, int T, int heads, int d,
@@ -1128,8 +1055,8 @@ extern "C" int clef_qk_norm_rotary_varlen(const void* x, int64_t ldx, int64_t hs
   RotaryTable tab{};
   for (int i = 0; i < rot_dim / 2; ++i)
     tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
-  if (qk_norm_rotary_tok_launch(QkSet{x, ldx, hs, w, y, ldy_tok, heads, dst_offset}, QkSet{}, dtype_in, dtype_out,
-                                T, d, rot_dim, pos0, eps, tab, cu_seqlens, nseq, static_cast<hipStream_t>(stream)))
+  if (qk_norm_rotary_tok_launch(x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d, rot_dim, pos0,
+                                dst_offset, eps, tab, cu_seqlens, nseq, static_cast<hipStream_t>(stream)))
     return check_launch("qk_norm_rotary");
   hipLaunchKernelGGL(qk_norm_rotary_kernel, dim3((T * heads + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, x, ldx, hs, dtype_in, w, y, ldy_tok, dtype_out, T, heads, d,
