@@ -597,6 +597,7 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   const int key_end = min(kn, offset + q0 + BQ);
   const int ntiles = (key_end + BK - 1) / BK;
   const int lim = min(offset + q0 + 16 * wave + n, kn1);
+  const int lim0 = min(offset + q0 + 16 * wave, kn1);  // the wave's smallest lim
   // key offset within a tile of accumulator element (t, i): LDS row
   // 16 t + 4 g + i holds key 32 (t / 2) + 8 g + 4 (t % 2) + i
   auto kof = [&](int t, int i) { return 32 * (t >> 1) + 4 * (t & 1) + i + 8 * g; };
@@ -645,7 +646,8 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   // K(j+1) and V(j) resident and the masked scores of tile j in Sc:
   //   phase 1: MFMA  Sn = K(j+1) Q^T        VALU  P = exp2(Sc c - m c), row sum
   //   phase 2: MFMA  O^T += V(j)^T P^T      VALU  mask Sn, row max of tile j+1
-  for (int j = 0; j < ntiles; ++j) {
+  auto tile_step = [&](int j, auto masked_t) {
+    constexpr bool masked = decltype(masked_t)::value;
     const int j0 = j * BK;
     if (j + 2 < ntiles) issue_k(j & 1, j0 + 2 * BK);
     if (j + 1 < ntiles) issue_v((j + 1) & 1, j0 + BK);
@@ -688,22 +690,33 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     // phase 2: one masked score of tile j+1 every second PV MFMA, two MFMAs
-    // behind the end of the score chain
+    // behind the end of the score chain (unmasked below the diagonal)
     auto mask_max = [&](int x) {
       const int t = x >> 2, i = x & 3;
       const float sv = kof(t, i) > thr ? -INFINITY : Sn[t][i];
       Sc[t][i] = sv;  // phase 1 is done with tile j's scores
       mx = fmaxf(mx, sv);
     };
+    auto max_only = [&](int x) {
+      const int t = x >> 2, i = x & 3;
+      Sc[t][i] = Sn[t][i];
+      mx = fmaxf(mx, Sn[t][i]);
+    };
+    auto phase2 = [&](auto&& scores) {
 #pragma unroll
-    for (int i = 0; i < NS2; ++i) {
-      O[i % NDT] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[(NS1 + i) % PD], pf[i / NDT], O[i % NDT], 0, 0, 0);
-      if (NS1 + i + PD < NS1 + NS2) fb[(NS1 + i) % PD] = frag(kbase, vbase, NS1 + i + PD);
-      if (i >= 2 && ((i - 2) & 1) == 0 && (i - 2) / 2 < 16) mask_max((i - 2) / 2);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int i = 0; i < NS2; ++i) {
+        O[i % NDT] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[(NS1 + i) % PD], pf[i / NDT], O[i % NDT], 0, 0, 0);
+        if (NS1 + i + PD < NS1 + NS2) fb[(NS1 + i) % PD] = frag(kbase, vbase, NS1 + i + PD);
+        if (i >= 2 && ((i - 2) & 1) == 0 && (i - 2) / 2 < 16) scores((i - 2) / 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-    for (int x = (NS2 - 2) / 2; x < 16; ++x) mask_max(x);
+      for (int x = (NS2 - 2) / 2; x < 16; ++x) scores(x);
+    };
+    if constexpr (masked)
+      phase2(mask_max);
+    else
+      phase2(max_only);
     l_run += ps;
     if (j + 1 < ntiles) {
       // lazy rescale: move the reference only when exp2 would exceed 2^8
@@ -718,7 +731,14 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
     }
     vm_wait_all();
     lds_barrier();
-  }
+  };
+  // single sequences: first the tiles whose successor lies wholly at or
+  // before the wave's first query (no mask), then the rest (a ragged batch's
+  // instance keeps one masked body: a second one costs it registers)
+  int j = 0;
+  if constexpr (!VL)
+    for (; j + 1 < ntiles && lim0 - (j + 1) * BK >= BK - 1; ++j) tile_step(j, std::false_type{});
+  for (; j < ntiles; ++j) tile_step(j, std::true_type{});
 
   // ---- epilogue: y = round(round(O / l) * round(sigmoid(gate))); O^T
   // accumulator t holds d = 16 t + 4 g + i of the lane's query
