@@ -73,6 +73,9 @@ SIGNATURES = {
     "clef_values_transposed": (_i, [_p, _l, _i, _p, _l, _i, _i, _i, _i, _i, _p]),
     "clef_attention_gated": (_i, [_p, _l, _p, _l, _p, _l, _i, _i, _i, _i, _i, _i, _p, _l, _l, _p, _l,
                                   _p]),
+    "clef_attention_gated_qnorm": (_i, [_p, _l, _l, _p, _f, _p, _p, _l, _p, _l, _i, _i, _i, _i, _i, _p, _l, _l,
+                                        _p, _l, _p]),
+    "clef_rotary_table": (_i, [_i, _i, _d, _i, _p, _p]),
     "clef_embed": (_i, [_p, _i, _p, _i, _i, _i, _p, _p]),
     "clef_head_logits": (_i, [_p, _i, _p, _i, _p, _p]),
 }
@@ -417,6 +420,27 @@ def attention_gated(q, k, vt, gate, kn=None):
     _check(lib().clef_attention_gated(_ptr(q), qn, _ptr(k), kn_, _ptr(vt), vt.shape[2], _dt(q), heads, kvh,
                                       qn, kn, d, _ptr(gate), gate.stride(0), gate.stride(1), _ptr(y),
                                       heads * d, _stream()))
+    return y
+
+
+def rotary_table(T, rot_dim, theta, pos0=0, device="cuda"):
+    """(cos, sin) of positions pos0 .. pos0 + T - 1 per rotary frequency: [T, rot_dim // 2, 2] f32."""
+    out = torch.empty((T, rot_dim // 2, 2), dtype=torch.float32, device=device)
+    _check(lib().clef_rotary_table(T, rot_dim, float(theta), pos0, _ptr(out), _stream()))
+    return out
+
+
+def attention_gated_qnorm(x, heads, w, eps, rot_tab, k, vt, gate, head_stride, kn=None):
+    """attention_gated of qk_norm_rotary(x) (rotary width 64, d = 256) with the query norm and
+    rotary inside the attention core: x [qn, *] raw query rows (head h at h * head_stride),
+    w [256] norm weights, rot_tab from rotary_table for the queries' positions."""
+    qn = x.shape[0]
+    kvh, kn_, d = k.shape
+    kn = kn or kn_
+    y = torch.empty((qn, heads * d), dtype=x.dtype, device=x.device)
+    _check(lib().clef_attention_gated_qnorm(_ptr(x), x.stride(0), head_stride, _ptr(w), float(eps), _ptr(rot_tab),
+                                            _ptr(k), kn_, _ptr(vt), vt.shape[2], heads, kvh, qn, kn, d, _ptr(gate),
+                                            gate.stride(0), gate.stride(1), _ptr(y), heads * d, _stream()))
     return y
 
 

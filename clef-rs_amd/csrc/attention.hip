@@ -259,6 +259,33 @@ extern "C" int clef_attention_gated(const void* q, int64_t ldq_tok, const void* 
   return clef::launch_d<float>(p, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int clef_attention_gated_qnorm(const void* q_raw, int64_t ldq_row, int64_t hsq, const float* q_norm,
+                                          float eps, const float* rot_tab, const void* k, int64_t ldk_tok,
+                                          const void* vt, int64_t ldv_tok, int heads, int kv_heads, int qn, int kn,
+                                          int d, const void* gate, int64_t ldg, int64_t hsg, void* y, int64_t ldy,
+                                          void* stream) {
+  CLEF_REQUIRE(q_raw && q_norm && rot_tab && k && vt && gate && y, "attention: null pointer");
+  CLEF_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "attention: head counts");
+  CLEF_REQUIRE(qn >= 1 && kn >= qn, "attention: causal attention needs 1 <= qn <= kn");
+  CLEF_REQUIRE(d == 256, "attention with the query norm: d = 256");
+  CLEF_REQUIRE(hsq >= d && ldq_row >= (int64_t)(heads - 1) * hsq + d, "attention: raw query strides");
+  CLEF_REQUIRE(ldk_tok >= kn && ldv_tok >= kn && ldv_tok % 8 == 0 && ldv_tok >= 64,
+               "attention: token strides (ldv_tok must be >= 64 and a multiple of 16 bytes)");
+  CLEF_REQUIRE(hsg >= d && ldg >= (int64_t)(heads - 1) * hsg + d && ldy >= (int64_t)heads * d,
+               "attention: gate or output strides");
+  clef::AttnParams p{q_raw, k, vt, gate, y, qn, ldk_tok, ldv_tok, ldg, hsg, ldy, heads, kv_heads, qn, kn, d,
+                     static_cast<float>(1.0 / std::sqrt(static_cast<double>(d)))};
+  p.qraw = q_raw;
+  p.ldqr = ldq_row;
+  p.hsr = hsq;
+  p.qw = q_norm;
+  p.qrot = reinterpret_cast<const float2*>(rot_tab);
+  p.qeps = eps;
+  p.qinv = static_cast<float>(1.0 / static_cast<double>(d));
+  CLEF_REQUIRE(clef::attn_qfuse_ok(p), "attention with the query norm: 16-byte aligned rows, weights and table");
+  return clef::attn_f16_launch(p, static_cast<hipStream_t>(stream));
+}
+
 extern "C" size_t clef_attention_varlen_workspace(int T, int nseq) {
   if (T < 1 || nseq < 1 || nseq > 4096) return 0;
   return clef::attn_tables_bytes(T, nseq);

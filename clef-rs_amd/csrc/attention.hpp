@@ -28,7 +28,20 @@ struct AttnParams {
   int64_t ldpk, ldpv;
   int np;
   int vec_io;        // set at launch: gate and y rows allow 8-byte accesses
+  // Fused query preparation (single sequences, f16, d = 256, rotary on 64
+  // features; null q-raw: q holds prepared rows).  Row t of head h is read
+  // at qraw + t * ldqr + h * hsr, RMS-normalised with weights qw (eps qeps,
+  // 1/d = qinv) and rotated by qrot[t] ([qn][32] (cos, sin) pairs), with the
+  // roundings of the per-token q/k norm + rotary kernel.
+  const void* qraw = nullptr;
+  int64_t ldqr = 0, hsr = 0;
+  const float* qw = nullptr;
+  const float2* qrot = nullptr;
+  float qeps = 0.0f, qinv = 0.0f;
 };
+
+// whether attn_f16_launch takes the fused query path for p (f16 data)
+bool attn_qfuse_ok(const AttnParams& p);
 
 // device tables of a ragged batch (workspace: attn_tables_bytes)
 size_t attn_tables_bytes(int T, int nseq);

@@ -441,6 +441,67 @@ __device__ __forceinline__ int key_perm16(int r) {
   return (r & ~31) | (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
 }
 
+// Fused query preparation for one query row t of head h, lane group g
+// holding features 32 s + 8 g .. + 7 (the Qᵀ fragments): the RMS norm and
+// rotary of the per-token q/k kernel (qwen.rs:451-470; pointwise.hip) with
+// its roundings and its association of the squares.  That kernel sums runs
+// of four consecutive features per lane, then an xor butterfly over the 64
+// runs with offsets 32, 16, 8, 4, 2, 1; here run L = 8 s + 2 g + u (u: the
+// fragment half), so offsets 32, 16, 8 pair runs inside a lane, 4 and 2 the
+// lane groups g ^ 2 and g ^ 1 (lanes 32 and 16 apart), and 1 the halves.
+// Rotary on features 0..63: feature i < 32 of fragment 0 pairs with i + 32
+// of fragment 1 in the same lane, by the (cos, sin) row of position t.
+__device__ __forceinline__ void q_prepare(const AttnParams& p, int t, int h, int g, half8* qf) {
+  constexpr int NKS = 8;
+  const half_t* src = static_cast<const half_t*>(p.qraw) + (int64_t)t * p.ldqr + (int64_t)h * p.hsr;
+  const float4_t* wp = reinterpret_cast<const float4_t*>(p.qw + 8 * g);
+  const float4_t* rt = reinterpret_cast<const float4_t*>(p.qrot + (int64_t)t * 32 + 8 * g);
+  // every load first (one memory latency): the row, its 64 weights, its 8 (cos, sin) pairs
+  float4_t wv[2 * NKS], cs[4];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) qf[s] = *reinterpret_cast<const half8*>(src + 32 * s + 8 * g);
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    wv[2 * s] = wp[8 * s];
+    wv[2 * s + 1] = wp[8 * s + 1];
+  }
+#pragma unroll
+  for (int e2 = 0; e2 < 4; ++e2) cs[e2] = rt[e2];  // features 8 g + 2 e2 and + 1
+  float tot[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float run[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = static_cast<float>(qf[s][4 * u + e]);
+        ss += v * v;
+      }
+      run[s] = ss;
+    }
+    const float b0 = run[0] + run[4], b1 = run[1] + run[5], b2 = run[2] + run[6], b3 = run[3] + run[7];
+    float x = (b0 + b2) + (b1 + b3);
+    x += __shfl_xor(x, 32, 64);
+    x += __shfl_xor(x, 16, 64);
+    tot[u] = x;
+  }
+  const float inverse = 1.0f / sqrtf(add_rn(mul_rn(tot[0] + tot[1], p.qinv), p.qeps));
+#pragma unroll
+  for (int s = 0; s < NKS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      qf[s][e] = to_f16(mul_rn(mul_rn(static_cast<float>(qf[s][e]), inverse), wv[2 * s + e / 4][e % 4]));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = cs[e / 2][2 * (e % 2)], sn = cs[e / 2][2 * (e % 2) + 1];
+    const float a = static_cast<float>(qf[0][e]), b = static_cast<float>(qf[1][e]);
+    qf[0][e] = to_f16(add_rn(mul_rn(a, c), mul_rn(b, -sn)));
+    qf[1][e] = to_f16(add_rn(mul_rn(b, c), mul_rn(a, sn)));
+  }
+}
+
 template <int D, bool VL>
 __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   constexpr int BQ = 128, BK = 64, NW = 8;
@@ -498,10 +559,19 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
   half8 qf[NKS];
   {
     const int r = min(q0 + 16 * wave + n, qn - 1);
+    bool prepared = false;
+    if constexpr (!VL) {
+      if (p.qraw) {  // raw projection rows: norm and rotary here (attn_qfuse_ok: d = 256)
+        q_prepare(p, r, h, g, qf);
+        prepared = true;
+      }
+    }
+    if (!prepared) {
 #pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-      const int c = 32 * s + 8 * g;
-      qf[s] = c < d ? *reinterpret_cast<const half8*>(Q + (int64_t)r * d + c) : half8{};
+      for (int s = 0; s < NKS; ++s) {
+        const int c = 32 * s + 8 * g;
+        qf[s] = c < d ? *reinterpret_cast<const half8*>(Q + (int64_t)r * d + c) : half8{};
+      }
     }
   }
 
@@ -917,7 +987,18 @@ bool attn_f16_ok(const AttnParams& p) {
          (int64_t)p.ldk * p.d < (int64_t(1) << 30) && (int64_t)p.d * p.ldv < (int64_t(1) << 30);
 }
 
+bool attn_qfuse_ok(const AttnParams& p) {
+  const auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  return kW8 && p.qraw && p.qw && p.qrot && !p.cu_q && p.d == 256 && attn_f16_ok(p) && a16(p.qraw) && a16(p.qw) &&
+         a16(p.qrot) && p.ldqr % 8 == 0 && p.hsr % 8 == 0 && p.hsr >= p.d &&
+         p.ldqr >= (int64_t)(p.heads - 1) * p.hsr + p.d;
+}
+
 int attn_f16_launch(const AttnParams& p, hipStream_t s) {
+  if (p.qraw) {
+    if (!attn_qfuse_ok(p)) return fail(-1, "attention: the fused query path takes one f16 sequence, d = 256 and aligned rows");
+    return launch_w8<256>(p, s);
+  }
   if (kW8 && p.d > 128) return launch_w8<256>(p, s);
   if (p.d <= 64) return launch<64>(p, s);
   if (p.d <= 128) return launch<128>(p, s);

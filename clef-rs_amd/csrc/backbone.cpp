@@ -123,6 +123,7 @@ struct Workspace {
   void* gated;    // [T, max(value, heads*d)] act
   void* mlp;      // [T, I] act
   void* qh;       // [heads, T, d] act
+  float* rot;     // [T, rotary_dim / 2] (cos, sin) pairs of the new tokens' positions
   void* kh;       // [kvh, Ttot, d] act
   void* vt;       // [kvh, d, ldv] act
   void* scan_ws;
@@ -180,6 +181,7 @@ size_t carve(const clef_backbone* b, int T, int prefix, Workspace* w, char* base
   W.gated = take(a * T * gated_cols);
   W.mlp = take(a * T * c.intermediate);
   W.qh = take(a * (size_t)c.heads * T * c.head_dim);
+  W.rot = static_cast<float*>(take(4ull * T * (c.rotary_dim > 0 ? c.rotary_dim : 2)));
   W.kh = take(a * (size_t)c.kv_heads * Ttot * c.head_dim);
   W.vt = take(a * (size_t)c.kv_heads * c.head_dim * ldv);
   W.scan_ws = take(scan_ws);
@@ -568,9 +570,15 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
       TIMED(CLEF_CAT_GEMM, 2.0 * T * NA * H, gemm_bytes(T, NA, H, false),
             clef_gemm(w.n, H, L.in_w, H, proj, NA, T, NA, H, ad, ad, CLEF_EPI_STORE, s));
       const size_t koff = a * 2 * heads * d, voff = koff + a * kvh * d;
-      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
-            clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim, c.rope_theta,
-                                offset, 0, c.eps, s));
+      // mixed profile, d = 256, rotary on 64 features: the query norm and
+      // rotary run inside the attention core (rotated by the key pass's
+      // table of the same positions); otherwise as their own pass
+      const bool qfuse = ad == CLEF_F16 && d == 256 && c.rotary_dim == 64 && NA % 8 == 0 &&
+                         ((reinterpret_cast<uintptr_t>(L.q_norm) | reinterpret_cast<uintptr_t>(proj)) & 15) == 0;
+      if (!qfuse)
+        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * heads * d,
+              clef_qk_norm_rotary(proj, NA, 2 * d, ad, L.q_norm, w.qh, T, ad, T, heads, d, c.rotary_dim,
+                                  c.rope_theta, offset, 0, c.eps, s));
       if (initial) {  // cached keys and values precede the new ones (qwen.rs:486-496)
         for (int g = 0; g < kvh; ++g)
           CLEF_TRY(copy_rows(static_cast<char*>(w.kh) + a * (size_t)g * Ttot * d,
@@ -579,9 +587,14 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
                                  hipMemcpyDeviceToDevice, s),
                 "value prefix copy");
       }
-      TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
-            clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
-                                c.rope_theta, offset, offset, c.eps, s));
+      if (qfuse)
+        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
+              qk_norm_rotary_table_launch(proj + koff, NA, d, L.k_norm, w.kh, Ttot, T, kvh, d, c.rotary_dim,
+                                          c.rope_theta, offset, offset, c.eps, w.rot, s));
+      else
+        TIMED(CLEF_CAT_NORM, 0, 2.0 * da * T * kvh * d,
+              clef_qk_norm_rotary(proj + koff, NA, d, ad, L.k_norm, w.kh, Ttot, ad, T, kvh, d, c.rotary_dim,
+                                  c.rope_theta, offset, offset, c.eps, s));
       TIMED(CLEF_CAT_OTHER, 0, 2.0 * da * T * kvh * d,
             clef_values_transposed(proj + voff, NA, ad, w.vt, w.ldv, ad, T, kvh, d, offset, s));
       if (capture) {
@@ -593,9 +606,14 @@ extern "C" int clef_backbone_prefill(clef_backbone* b, const int32_t* ids, int T
                 "value capture");
       }
       const double pairs = static_cast<double>(T) * offset + 0.5 * T * (T + 1.0);
-      TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pairs, da * (3.0 * T * heads * d + 2.0 * Ttot * kvh * d),
-            clef_attention_gated(w.qh, T, w.kh, Ttot, w.vt, w.ldv, ad, heads, kvh, T, Ttot, d, proj + a * d, NA,
-                                 2 * d, w.gated, (int64_t)heads * d, s));
+      if (qfuse)
+        TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pairs, da * (3.0 * T * heads * d + 2.0 * Ttot * kvh * d),
+              clef_attention_gated_qnorm(proj, NA, 2 * d, L.q_norm, c.eps, w.rot, w.kh, Ttot, w.vt, w.ldv, heads,
+                                         kvh, T, Ttot, d, proj + a * d, NA, 2 * d, w.gated, (int64_t)heads * d, s));
+      else
+        TIMED(CLEF_CAT_ATTENTION, 4.0 * d * heads * pairs, da * (3.0 * T * heads * d + 2.0 * Ttot * kvh * d),
+              clef_attention_gated(w.qh, T, w.kh, Ttot, w.vt, w.ldv, ad, heads, kvh, T, Ttot, d, proj + a * d, NA,
+                                   2 * d, w.gated, (int64_t)heads * d, s));
       TIMED(CLEF_CAT_GEMM, 2.0 * T * H * heads * d, gemm_bytes(T, H, heads * d, true),
             clef_gemm(w.gated, heads * d, L.out, heads * d, h, H, T, H, heads * d, ad, ad, CLEF_EPI_RESIDUAL, s));
     }

@@ -168,6 +168,14 @@ bool embed_rms_applies(const void* table, int H, const float* h, const float* w,
 int embed_rms_launch(const int32_t* ids, int T, const void* table, int dtype_table, int vocab, int H, float* h,
                      const float* w, void* y, int64_t ldy, int dtype_out, float eps, hipStream_t st);
 
+// Key norm + rotary (f16) that also writes the (cos, sin) rows of positions
+// pos0 .. pos0 + T - 1 to tab_out ([T][rot / 2] float2) for the attention
+// core's fused query path (pointwise.hip); an error, nothing launched, off
+// the per-token kernel's shapes.
+int qk_norm_rotary_table_launch(const void* x, int64_t ldx, int64_t hs, const float* w, void* y, int64_t ldy_tok,
+                                int T, int heads, int d, int rot, double theta, int pos0, int dst_offset, float eps,
+                                float* tab_out, hipStream_t st);
+
 }  // namespace clef
 
 #define CLEF_REQUIRE(cond, msg)                              \

@@ -554,6 +554,14 @@ struct RotaryTable {
   float inv_freq[128];
 };
 
+// cos and sin of position p times one inverse frequency (ops.rs:165-188):
+// the angle rounded once in f32, then the library cosf / sinf
+__device__ __forceinline__ void rotary_angle(float p, float inv_freq, float& c, float& s) {
+  const float ang = mul_rn(p, inv_freq);
+  c = cosf(ang);
+  s = sinf(ang);
+}
+
 __global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const void* x, int64_t ldx, int64_t hs,
                                                              int dti, const float* w, void* y,
                                                              int64_t ldy_tok, int dto, int T,
@@ -603,7 +611,8 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
                                                           const float* __restrict__ w, TO* __restrict__ y,
                                                           int64_t ldy_tok, int heads, int rot, int pos0,
                                                           int dst_offset, float eps, float inv_width, int vec,
-                                                          RotaryTable tab, const int* __restrict__ cu, int nseq) {
+                                                          RotaryTable tab, const int* __restrict__ cu, int nseq,
+                                                          float2* __restrict__ tab_out) {
   constexpr int D = 64 * EPL;
   __shared__ float cs[128], sn[128];
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -611,9 +620,8 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
   // position: pos0 + t, or pos0 + (t - first token of t's sequence)
   const float p = static_cast<float>(pos0 + (cu ? t - seq_start(cu, nseq, t) : t));
   for (int f = threadIdx.x; f < half; f += 256) {
-    const float ang = mul_rn(p, tab.inv_freq[f]);
-    cs[f] = cosf(ang);
-    sn[f] = sinf(ang);
+    rotary_angle(p, tab.inv_freq[f], cs[f], sn[f]);
+    if (tab_out) tab_out[(int64_t)t * half + f] = make_float2(cs[f], sn[f]);
   }
   __syncthreads();
   const int i0 = lane * EPL;
@@ -980,7 +988,7 @@ extern "C" int clef_gated_rms_silu(const void* o, int dtype_o, const void* z, in
 static bool qk_norm_rotary_tok_launch(const void* x, int64_t ldx, int64_t hs, int dti, const float* w, void* y,
                                       int64_t ldy_tok, int dto, int T, int heads, int d, int rot, int pos0,
                                       int dst_offset, float eps, const RotaryTable& tab, const int* cu, int nseq,
-                                      hipStream_t st) {
+                                      hipStream_t st, float2* tab_out = nullptr) {
   const int epl = d / 64;
   if (d % 64 != 0 || !(epl == 1 || epl == 2 || epl == 4) || (rot / 2) % epl != 0) return false;
   const int es_in = dti == CLEF_F16 ? 2 : 4, es_out = dto == CLEF_F16 ? 2 : 4;
@@ -991,7 +999,8 @@ static bool qk_norm_rotary_tok_launch(const void* x, int64_t ldx, int64_t hs, in
   const float inv = static_cast<float>(1.0 / static_cast<double>(d));
 #define CLEF_QKR(E, TI, TO)                                                                                     \
   hipLaunchKernelGGL((qk_norm_rotary_tok<E, TI, TO>), dim3(T), dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
-                     hs, w, static_cast<TO*>(y), ldy_tok, heads, rot, pos0, dst_offset, eps, inv, vec, tab, cu, nseq)
+                     hs, w, static_cast<TO*>(y), ldy_tok, heads, rot, pos0, dst_offset, eps, inv, vec, tab, cu, nseq, \
+                     tab_out)
 #define CLEF_QKR_E(TI, TO)      \
   if (epl == 4)                 \
     CLEF_QKR(4, TI, TO);        \
@@ -1063,6 +1072,51 @@ extern "C" int clef_qk_norm_rotary_varlen(const void* x, int64_t ldx, int64_t hs
                      rot_dim, pos0, dst_offset, eps, static_cast<float>(1.0 / static_cast<double>(d)),
                      tab, cu_seqlens, nseq);
   return check_launch("qk_norm_rotary");
+}
+
+// (cos, sin) of positions pos0 + t for the rot / 2 rotary frequencies, as
+// float2 rows [T][rot / 2]: the values the per-token q/k kernel rotates by.
+__global__ __launch_bounds__(64) void rotary_table_kernel(RotaryTable tab, int half, int pos0, float2* __restrict__ out) {
+  const int t = blockIdx.x;
+  const float p = static_cast<float>(pos0 + t);
+  for (int f = threadIdx.x; f < half; f += 64) {
+    float c, s;
+    rotary_angle(p, tab.inv_freq[f], c, s);
+    out[(int64_t)t * half + f] = make_float2(c, s);
+  }
+}
+
+namespace clef {
+// The key norm + rotary of the single-sequence attention layer, also writing
+// the (cos, sin) rows of its positions to tab_out ([T][rot / 2] float2) for
+// the attention core's fused query preparation (f16 in and out; the
+// per-token kernel's shapes: an error, before any launch, elsewhere).
+int qk_norm_rotary_table_launch(const void* x, int64_t ldx, int64_t hs, const float* w, void* y, int64_t ldy_tok,
+                                int T, int heads, int d, int rot, double theta, int pos0, int dst_offset, float eps,
+                                float* tab_out, hipStream_t st) {
+  CLEF_REQUIRE(x && w && y && tab_out && T >= 1 && heads >= 1 && rot >= 2 && rot <= d && rot % 2 == 0 &&
+                   rot / 2 <= 128 && hs >= d && ldy_tok >= (int64_t)dst_offset + T && pos0 >= 0,
+               "q/k norm with rotary table: arguments");
+  RotaryTable tab{};
+  for (int i = 0; i < rot / 2; ++i)  // ops.rs:165, as clef_qk_norm_rotary
+    tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot));
+  if (!qk_norm_rotary_tok_launch(x, ldx, hs, CLEF_F16, w, y, ldy_tok, CLEF_F16, T, heads, d, rot, pos0, dst_offset,
+                                 eps, tab, nullptr, 0, st, reinterpret_cast<float2*>(tab_out)))
+    return fail(-1, "q/k norm with rotary table: d must be 64, 128 or 256 with whole lanes of the rotary half");
+  return check_launch("qk_norm_rotary");
+}
+}  // namespace clef
+
+extern "C" int clef_rotary_table(int T, int rot_dim, double theta, int pos0, float* out, void* stream) {
+  CLEF_REQUIRE(out, "rotary table: null pointer");
+  CLEF_REQUIRE(T >= 1 && rot_dim >= 2 && rot_dim % 2 == 0 && rot_dim / 2 <= 128 && pos0 >= 0,
+               "rotary table: dimensions");
+  RotaryTable tab{};
+  for (int i = 0; i < rot_dim / 2; ++i)  // ops.rs:165, as clef_qk_norm_rotary
+    tab.inv_freq[i] = static_cast<float>(std::pow(theta, -static_cast<double>(2 * i) / rot_dim));
+  hipLaunchKernelGGL(rotary_table_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, tab, rot_dim / 2, pos0,
+                     reinterpret_cast<float2*>(out));
+  return check_launch("rotary_table");
 }
 
 extern "C" int clef_values_transposed(const void* x, int64_t ldx, int dtype_in, void* y, int64_t ldy_tok,

@@ -289,6 +289,29 @@ int clef_attention_gated(const void* q, int64_t ldq_tok, const void* k, int64_t 
                          int qn, int kn, int d, const void* gate, int64_t ldg, int64_t hsg,
                          void* y, int64_t ldy, void* stream);
 /*
+ * clef_attention_gated with the query RMS norm and rotary of qwen.rs:459-468
+ * (as clef_qk_norm_rotary computes them, bit for bit) folded into the
+ * attention core's query loads: row t of head h is read raw, f16, at
+ * q_raw + t * ldq_row + h * hsq, normalised with q_norm (d weights, eps) and
+ * rotated on its first 64 features by rot_tab row t (the cos, sin pairs of
+ * clef_rotary_table for the same positions).  One f16 sequence, d = 256,
+ * rotary width 64, 16-byte aligned rows, weights and table.  No counterpart
+ * in the reference (there the norm and rotary are their own passes); it
+ * saves the query pass of clef_qk_norm_rotary and its [heads, qn, d] copy.
+ */
+int clef_attention_gated_qnorm(const void* q_raw, int64_t ldq_row, int64_t hsq, const float* q_norm, float eps,
+                               const float* rot_tab, const void* k, int64_t ldk_tok, const void* vt,
+                               int64_t ldv_tok, int heads, int kv_heads, int qn, int kn, int d, const void* gate,
+                               int64_t ldg, int64_t hsg, void* y, int64_t ldy, void* stream);
+/*
+ * The rotary (cos, sin) pairs of positions pos0 .. pos0 + T - 1, as
+ * clef_qk_norm_rotary forms them (ops.rs:165-188: the angle rounded once in
+ * f32, then cos and sin), written as out[t][i] = {cos, sin} of frequency i
+ * < rot_dim / 2 (float pairs, [T][rot_dim / 2][2]).  The table of
+ * clef_attention_gated_qnorm.
+ */
+int clef_rotary_table(int T, int rot_dim, double theta, int pos0, float* out, void* stream);
+/*
  * Ragged batch (mixed profile, dtype f16): sequence s owns packed rows
  * cu_seqlens[s] .. cu_seqlens[s+1]-1 (device int32, nseq + 1 offsets in
  * [0, T]) of q [heads, ldq_tok, d], k [kv_heads, ldk_tok, d], vt

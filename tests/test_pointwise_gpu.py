@@ -159,6 +159,56 @@ def test_qk_norm_rotary_matches_oracle(clef, dt, heads, d, rot, pos0):
 
 
 @gpu
+@pytest.mark.parametrize("heads,kvh,qn,kn", [(16, 2, 300, 300), (16, 2, 4096, 4096), (4, 2, 130, 642),
+                                             (2, 1, 1, 256), (8, 8, 65, 65)])
+def test_attention_with_query_norm_equals_norm_then_attention(clef, heads, kvh, qn, kn):
+    """The query RMS norm + rotary (qwen.rs:459-468) inside the attention core
+    equals clef_qk_norm_rotary followed by clef_attention_gated bit for bit,
+    with the queries at positions kn - qn .. kn - 1 as in a resumed prefill;
+    the rotary table equals the angles clef_qk_norm_rotary rotates by."""
+    d, rot, theta, eps = 256, 64, 1e7, 1e-6
+    gen = torch.Generator(device="cuda").manual_seed(qn + 3 * kn)
+    proj = (2.0 * torch.randn((qn, heads, 2 * d), generator=gen, device="cuda")).half()
+    x = proj.reshape(qn, heads * 2 * d)
+    w = 1.0 + 0.1 * torch.randn((d,), generator=gen, device="cuda")
+    k = torch.randn((kvh, kn, d), generator=gen, device="cuda").half()
+    v = torch.randn((kvh, kn, d), generator=gen, device="cuda").half()
+    vt = clef.values_transposed(v.permute(1, 0, 2).contiguous().reshape(kn, kvh * d), kvh, d)
+    gate = proj[:, :, d:]
+    pos0 = kn - qn
+    q = clef.qk_norm_rotary(x, heads, d, w, rot, theta, pos0=pos0, head_stride=2 * d, eps=eps)
+    ref = clef.attention_gated(q, k, vt, gate)
+    tab = clef.rotary_table(qn, rot, theta, pos0=pos0)
+    got = clef.attention_gated_qnorm(x, heads, w, eps, tab, k, vt, gate, 2 * d)
+    assert torch.equal(got, ref)
+    ang = (np.arange(pos0, pos0 + qn, dtype=np.float64)[:, None]
+           * (theta ** (-np.arange(0, rot, 2, dtype=np.float64) / rot)).astype(np.float32)[None, :])
+    t = tab.cpu().numpy()
+    np.testing.assert_allclose(t[:, :, 0], np.cos(ang.astype(np.float32)), rtol=0, atol=2e-6)
+    np.testing.assert_allclose(t[:, :, 1], np.sin(ang.astype(np.float32)), rtol=0, atol=2e-6)
+
+
+@gpu
+def test_attention_with_query_norm_rejects_other_shapes(clef):
+    """d other than 256, or a misaligned head stride: an error before launch."""
+    heads, kvh, qn, d = 2, 1, 8, 128
+    x = torch.zeros((qn, heads * 2 * d), dtype=torch.float16, device="cuda")
+    w = torch.ones((d,), device="cuda")
+    k = torch.zeros((kvh, qn, d), dtype=torch.float16, device="cuda")
+    vt = torch.zeros((kvh, d, 64), dtype=torch.float16, device="cuda")
+    tab = clef.rotary_table(qn, 64, 1e7)
+    with pytest.raises(clef.ClefError):
+        clef.attention_gated_qnorm(x, heads, w, 1e-6, tab, k, vt, x.view(qn, heads, 2 * d)[:, :, d:], 2 * d)
+    x2 = torch.zeros((qn, heads * 2 * 256 + 4), dtype=torch.float16, device="cuda")
+    w2 = torch.ones((256,), device="cuda")
+    k2 = torch.zeros((kvh, qn, 256), dtype=torch.float16, device="cuda")
+    vt2 = torch.zeros((kvh, 256, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(clef.ClefError):  # head stride 516 halves: rows not 16-byte aligned
+        clef.attention_gated_qnorm(x2, heads, w2, 1e-6, tab, k2, vt2, x2[:, :heads * 256].view(qn, heads, 256),
+                                   516)
+
+
+@gpu
 def test_delta_gates_matches_reference_formula(clef):
     T, Hv = 333, 32
     gen = torch.Generator(device="cuda").manual_seed(2)
