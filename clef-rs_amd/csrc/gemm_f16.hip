@@ -5,10 +5,11 @@
 //
 // A work-group of 8 waves (4 x 2, two per SIMD) computes a 256 x BN tile
 // (or 128 x BN when 256-row tiles would leave CUs idle), each wave
-// BM/4 x BN/2 with v_mfma_f32_32x32x16_f16 (at most 128 accumulator
-// registers per wave, which the register allocator keeps in place).  K
-// advances in 64-element stages through LDS rings filled by global->LDS DMA
-// (global_load_lds_dwordx4, 1 KiB per wave instruction): three slots per
+// BM/4 x BN/2 as 16 x 16 blocks on v_mfma_f32_16x16x32_f16 (at most 128
+// accumulator registers per wave, which the register allocator keeps in
+// place).  K advances in 64-element stages (two 32-deep k-steps) through LDS
+// rings filled by global->LDS DMA (buffer_load_dwordx4 ... lds, 1 KiB per
+// wave instruction): three slots per
 // operand for 128-wide tiles, two activation and three weight slots for
 // wider ones, so a stage's weights land two stages ahead of their use.
 // Rows are 128 bytes; the 16-byte chunk c of row r is stored at slot
@@ -19,10 +20,14 @@
 // 256 x 256 tiles run on gemm_f16_w4 instead: four waves (one per SIMD,
 // 128 x 128 each, 256 accumulator registers) whose products, fragment reads
 // and DMA are interleaved in a fixed order, one MFMA at a time; the same
-// rings, layout and epilogue arithmetic, so the results are bit-identical.
-// At 4096 x 12288 x 2048 the matrix cores are busy 0.66 of the time against
-// 0.54 with eight compiler-scheduled waves (in-projection 186 -> 177 us and
-// SwiGLU 188 -> 182 us over 200 back-to-back calls).
+// rings, layout, products and epilogue arithmetic, so the results are
+// bit-identical.  At 4096 x 12288 x 2048 the matrix cores are busy 0.66 of
+// the time against 0.54 with eight compiler-scheduled waves.  Both kernels
+// multiply on 16 x 16 x 32 products: on the 256 x 256 tiles they took the
+// in-projection from 183.7 to 172.5 us against 32 x 32 x 16 ones (same
+// fragment bytes per stage: twice the products, each half as long, so a
+// fragment read or DMA request sits beside every second product instead of
+// most of them).
 #include <algorithm>
 #include <utility>
 
@@ -86,7 +91,8 @@ template <int BM, int BN, int VM, int NSA, int NSB, int EPI, bool PERSIST>
 __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int kWaves = VM * 2;  // VM wave rows x 2 wave columns
   constexpr int WM = BM / VM, WN = BN / 2;
-  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int TM = WM / 32;                    // 32-row slabs of the epilogue per wave
+  constexpr int TM16 = WM / 16, TN16 = WN / 16;  // 16 x 16 product blocks per wave
   constexpr int NA = BM * 8 / 64 / kWaves;  // A DMA instructions per wave per stage
   constexpr int NB = BN * 8 / 64 / kWaves;
   typedef half8 frag;
@@ -166,45 +172,46 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     }
   };
 
-  float16_t acc[TM][TN];
+  // Products on v_mfma_f32_16x16x32_f16 (the four-wave kernel's, so both
+  // kernels sum every output in the same order): acc[I][J] holds rows
+  // 16 I + 4 (lane / 16) + e, column 16 J + lane % 16 of the wave's block.
+  float4_t acc[TM16][TN16];
 
-  // fragment reads: row r = (wave offset) + 32 i + lane % 32 has swizzle key
-  // (lane % 32 >> 1) & 7, so a lane's byte offset within any 32-row block is
-  // one of four values (k-block kb); the block offsets are immediates
-  const int frow = lane & 31, fkc = lane >> 5;
-  int foff[4];
+  // fragment reads: row r = (wave offset) + 16 i + lane % 16, 16-byte chunk
+  // 4 ks + lane / 16 of k-step ks, at chunk ^ ((r >> 1) & 7); the row's key
+  // is (lane % 16 >> 1) & 7, so a lane's byte offset within any 16-row block
+  // is one of two values (k-step ks); the block offsets are immediates
+  const int r16 = lane & 15, c16 = lane >> 4;
+  int goff[2];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) foff[kb] = 2 * (frow * kBK + (((2 * kb + fkc) ^ ((frow >> 1) & 7)) << 3));
-  // k-block kb+1's fragments are requested during kb's products; dma(kb)
-  // issues part kb of a later stage's DMA before them
+  for (int ks = 0; ks < 2; ++ks) goff[ks] = 2 * (r16 * kBK + (((4 * ks + c16) ^ ((r16 >> 1) & 7)) << 3));
+  // k-step 1's fragments are requested during k-step 0's products; dma(ks)
+  // issues part ks of a later stage's DMA before them
   auto compute = [&](const half_t* sa, const half_t* sb, auto&& dma) {
     const char* ab = reinterpret_cast<const char*>(sa) + wm * WM * kBK * 2;
     const char* bb = reinterpret_cast<const char*>(sb) + wn * WN * kBK * 2;
-    frag af[2][TM], bf[2][TN];
-    auto load = [&](int kb) {
+    frag af[2][TM16], bf[2][TN16];
+    auto load = [&](int ks) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[kb & 1][i] = *reinterpret_cast<const frag*>(ab + foff[kb] + i * 32 * kBK * 2);
+      for (int i = 0; i < TM16; ++i) af[ks][i] = *reinterpret_cast<const frag*>(ab + goff[ks] + i * 16 * kBK * 2);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[kb & 1][j] = *reinterpret_cast<const frag*>(bb + foff[kb] + j * 32 * kBK * 2);
+      for (int j = 0; j < TN16; ++j) bf[ks][j] = *reinterpret_cast<const frag*>(bb + goff[ks] + j * 16 * kBK * 2);
     };
     load(0);
 #pragma unroll
-    for (int kb = 0; kb < kBK / 16; ++kb) {
-      dma(kb);
-      if (kb + 1 < kBK / 16) load(kb + 1);
+    for (int ks = 0; ks < 2; ++ks) {
+      dma(ks);
+      if (ks == 0) load(1);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM16; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kb & 1][i], bf[kb & 1][j], acc[i][j], 0, 0, 0);
-      // one fragment read of k-block kb+1 after each product of kb, so the
+        for (int j = 0; j < TN16; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+      // one fragment read of k-step 1 after each product of k-step 0, so the
       // reads stream under the products and are in long before their use
-      // (the compiler otherwise issues them late and waits on them; 2-5%
-      // faster on the in-projection and SwiGLU shapes with the weights
-      // cache-resident, neutral in a whole prefill; bit-identical)
-      if (kb + 1 < kBK / 16) {
+      if (ks == 0) {
 #pragma unroll
-        for (int q = 0; q < TM + TN; ++q) {
+        for (int q = 0; q < TM16 + TN16; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
         }
@@ -272,11 +279,9 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     if (next) coords(ntile, nm0, nn0);
     const bool pf = PF && yvec && nk >= kPD && m0 + BM <= p.M && n0 + BN <= p.N;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM16; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+      for (int j = 0; j < TN16; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
     // requests stage ks of this tile or, past its end, of the next one
     auto issue_at = [&](half_t* sa, half_t* sb, int ks, int part = 0, int nparts = 1) {
       if (ks < nk)
@@ -340,13 +345,15 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
                     "f16 staging of four waves fits a stage slot");
       const int pa = ca == 0 ? NSA - 1 : ca - 1, pb = cb == 0 ? NSB - 1 : cb - 1;
       half_t* const stg = (wave < 4 ? sA(pa) : sB(pb)) + (wave & 3) * (32 * WN);
-      const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+      const int scol = lane & 15, srow = (lane >> 4) * 4;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
+      for (int i = 0; i < TM; ++i) {  // slab i: product block rows 2 i and 2 i + 1
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = to_f16(acc[i][j][e]);
+          for (int j = 0; j < TN16; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * WN + j * 16 + scol] = to_f16(acc[2 * i + h][j][e]);
         const int rbase = m0 + wm * WM + i * 32;
         const int cbase = n0 + wn * OW;
 #pragma unroll
@@ -386,19 +393,20 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
 
     // ---- epilogue.  The loop's last barrier follows every wave's last
     // fragment read, so each wave now owns a 32 x WN f32 staging block.
-    // acc[i][j][e] holds row (e/4)*8 + (lane/32)*4 + e%4, column lane%32 of
-    // 32 x 32 block (i, j); a 32-row slab is written there and read back as
-    // 4-column chunks, so the global accesses are 8- or 16-byte vectors along
-    // the rows.  (LDS operations of one wave complete in order, so the
-    // write -> read -> next write sequence needs no barrier.)
+    // A 32-row slab (product block rows 2 i and 2 i + 1) is written there
+    // and read back as 4-column chunks, so the global accesses are 8- or
+    // 16-byte vectors along the rows.  (LDS operations of one wave complete
+    // in order, so the write -> read -> next write sequence needs no barrier.)
     float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
-    const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+    const int scol = lane & 15, srow = (lane >> 4) * 4;
   #pragma unroll
     for (int i = 0; i < TM; ++i) {
   #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int h = 0; h < 2; ++h)
   #pragma unroll
-        for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = acc[i][j][e];
+        for (int j = 0; j < TN16; ++j)
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * WN + j * 16 + scol] = acc[2 * i + h][j][e];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
       float4 v[PER], res[PER];
@@ -485,20 +493,20 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   }
 }
 
-// ---- 256 x 256 tiles on four waves (one per SIMD, 128 x 128 each, 256
-// accumulator registers), with the stage's products, its fragment reads and
-// the DMA of the stage two ahead interleaved by hand: the compiler's own
-// schedule of the eight-wave kernel leaves the matrix cores idle while both
-// waves of a SIMD wait on LDS.  Same rings (A: 2 stages, B: 3), swizzle,
-// tile order and epilogue arithmetic as gemm_f16_dma, so results are
-// bit-identical to it.
+// ---- 256 x 256 tiles on four waves (one per SIMD, 128 x 128 each as 8 x 8
+// blocks of 16 x 16, 256 accumulator registers), with the stage's products,
+// its fragment reads and the DMA of the stage two ahead interleaved by hand:
+// the compiler's own schedule of the eight-wave kernel leaves the matrix
+// cores idle while both waves of a SIMD wait on LDS.  Same rings (A: 2
+// stages, B: 3), swizzle, tile order, products and epilogue arithmetic as
+// gemm_f16_dma, so results are bit-identical to it.
 template <int EPI, bool PERSIST>
 __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   constexpr int BM = 256, BN = 256, VM = 2;
   constexpr int kWaves = VM * 2;
   constexpr int WM = BM / VM, WN = BN / 2, TM = WM / 32, TN = WN / 32;
   constexpr int NA = BM * 8 / 64 / kWaves, NB = BN * 8 / 64 / kWaves;  // 8 DMA instructions each
-  static_assert(TM == 4 && TN == 4 && NA == 8 && NB == 8, "the hand schedule below assumes 4 x 4 blocks");
+  static_assert(TM == 4 && TN == 4 && NA == 8 && NB == 8, "the hand schedule below assumes 128 x 128 per wave");
   typedef half8 frag;
   constexpr int kStA = BM * kBK, kStB = BN * kBK;
   __shared__ __attribute__((aligned(1024))) half_t smem[2 * kStA + 3 * kStB];
@@ -556,21 +564,28 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
     bdma16(rB, (uint32_t)(nr * (int)p.ldw + lcol[j & 1] + ks * kBK) * 2u, sB(slot) + j * 512);
   };
 
-  // fragment q of a k-block: A blocks 0..3, then B blocks 4..7
-  const int frow = lane & 31, fkc = lane >> 5;
-  int foff[4];
+  // Products on v_mfma_f32_16x16x32_f16: the wave's 128 x 128 as 8 x 8
+  // blocks of 16 x 16, a stage as two 32-deep k-steps.  Fragment of block I
+  // at k-step ks: lane l holds row 16 I + l % 16, k 32 ks + 8 (l / 16) .. + 7
+  // (16 rows x 4 chunks per read: with the (row >> 1) & 7 swizzle, every 16
+  // lanes of a read cover all 64 banks).  A block I is read into FA[I] once
+  // its eight products of the current k-step are issued; B blocks into the
+  // other half of FB.
+  const int r16 = lane & 15, c16 = lane >> 4;
+  int goff[2];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) foff[kb] = 2 * (frow * kBK + (((2 * kb + fkc) ^ ((frow >> 1) & 7)) << 3));
-  frag F[2][TM + TN];
-  auto rd = [&](frag* f, int sa, int sb, int kb, int q) {
-    if (q < TM)
-      f[q] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sA(sa)) + wm * WM * kBK * 2 + foff[kb] +
-                                            q * 32 * kBK * 2);
+  for (int ks = 0; ks < 2; ++ks) goff[ks] = 2 * (r16 * kBK + (((4 * ks + c16) ^ ((r16 >> 1) & 7)) << 3));
+  frag FA[8], FB[2][8];
+  auto rd = [&](int sa, int sb, int ks, int q, int fb) {  // q < 8: A block q, else B block q - 8 into FB[fb]
+    if (q < 8)
+      FA[q] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sA(sa)) + wm * WM * kBK * 2 + goff[ks] +
+                                             q * 16 * kBK * 2);
     else
-      f[q] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sB(sb)) + wn * WN * kBK * 2 + foff[kb] +
-                                            (q - TM) * 32 * kBK * 2);
+      FB[fb][q - 8] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sB(sb)) + wn * WN * kBK * 2 +
+                                                     goff[ks] + (q - 8) * 16 * kBK * 2);
   };
-  float16_t acc[TM][TN];
+  // acc[I][J] holds rows 16 I + 4 (lane / 16) + e, column 16 J + lane % 16
+  float4_t acc[8][8];
 
   const int nk = p.K / kBK;
   // prologue: stages 0 and 1 requested, stage 0 published, its first k-block
@@ -591,15 +606,16 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   }
   lds_barrier();
 #pragma unroll
-  for (int q = 0; q < TM + TN; ++q) rd(F[0], 0, 0, 0, q);
+  for (int q = 0; q < 16; ++q) rd(0, 0, 0, q, 0);
 
-  // One stage: 4 k-blocks x 16 products.  During k-blocks 0-2, the first 8
-  // products each carry one fragment read of the next k-block; during
-  // k-blocks 0-1, 8 later products carry the DMA of B two stages ahead (into
-  // the slot stage s-1 freed).  In k-block 3 (its fragments already in
-  // registers) the wave waits for its own requests of stage s+1, the barrier
-  // publishes them and frees stage s's A slot, and products 4-11 each carry
-  // one fragment read of stage s+1 and one DMA of A two stages ahead.
+  // One stage: 2 k-steps x 64 products (block row I outer, column J inner).
+  // In k-step 0 the products carry k-step 1's fragment reads (B during the
+  // first 16, A block I after its last product) and, from product 17, the
+  // DMA of B two stages ahead (into the slot stage s-1 freed), one per four.
+  // In k-step 1 the wave waits at product 6 for its own requests of stage
+  // s+1, the barrier publishes them and frees stage s's A slot, and the
+  // products carry stage s+1's first fragment reads and, from product 9, the
+  // DMA of A two stages ahead.
   // has1 / has2: stages s+1 / s+2 exist (compile-time, so the steady state
   // has no branches between its instructions); the stage-(s+2) requests go
   // to tile (tm2, tn2) at k-stage ks2.
@@ -609,19 +625,18 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
     const int na2 = ca, nb2 = cb == 0 ? 2 : cb - 1;      // slots of A(s+2) and B(s+2)
     const int ca1 = ca ^ 1, cb1 = cb == 2 ? 0 : cb + 1;  // slots of stage s+1
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      frag* cur = F[kb & 1];
-      frag* nxt = F[(kb + 1) & 1];
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int i = m >> 2, j = m & 3;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[i], cur[TM + j], acc[i][j], 0, 0, 0);
+      for (int m = 0; m < 64; ++m) {
+        const int I = m >> 3, J = m & 7;
+        acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(FA[I], FB[ks][J], acc[I][J], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if (kb < 3) {
-          if (m < 8) rd(nxt, ca, cb, kb + 1, m);
-          if (kb < 2 && m >= 9 && (m & 1) && has2) dma_b(nb2, tn2, ks2, kb * 4 + ((m - 9) >> 1));
+        if (ks == 0) {
+          if ((m & 7) == 7) rd(ca, cb, 1, I, 0);
+          if (m < 16 && (m & 1)) rd(ca, cb, 1, 8 + (m >> 1), 1);
+          if (m >= 17 && m < 49 && ((m - 17) & 3) == 0 && has2) dma_b(nb2, tn2, ks2, (m - 17) >> 2);
         } else {
-          if (m == 3 && has1) {
+          if (m == 6 && has1) {
             // in flight after stage s+1's requests: B(s+2) only
             if (has2)
               vm_wait<NB>();
@@ -629,9 +644,10 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
               vm_wait_all();
             lds_barrier();
           }
-          if (m >= 4 && m < 12 && has1) {
-            rd(nxt, ca1, cb1, 0, m - 4);
-            if (has2) dma_a(na2, tm2, ks2, m - 4);
+          if (has1) {
+            if ((m & 7) == 7) rd(ca1, cb1, 0, I, 0);
+            if (m >= 8 && m < 24 && (m & 1)) rd(ca1, cb1, 0, 8 + ((m - 8) >> 1), 0);
+            if (m >= 9 && m < 41 && ((m - 9) & 3) == 0 && has2) dma_a(na2, tm2, ks2, (m - 9) >> 2);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -647,14 +663,12 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
   constexpr int OW = EPI == 2 ? WN / 2 : WN;  // output columns per wave
   constexpr int CPR = OW / 4, PER = 32 * CPR / 64;
-  const int ccol = lane & 31, rgrp = (lane >> 5) * 4;
+  const int scol = lane & 15, srow = (lane >> 4) * 4;
   auto zero = [&] {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+      for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   };
 
   if constexpr (PERSIST) {
@@ -677,17 +691,19 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       // passed that stage's barrier, and the next request into it is the
       // next tile's B(2)); each wave stages its 32 x WN slabs there in f16,
       // rounded once as the stores would be, and as SwiGLU rounds gate and
-      // up before combining them (neural.metal:35-42).  acc[i][j][e] holds
-      // row (e/4)*8 + (lane/32)*4 + e%4, column lane%32 of block (i, j).
+      // up before combining them (neural.metal:35-42).  Slab i holds the
+      // 16-row blocks 2 i and 2 i + 1.
       const int lastb = cb == 0 ? 2 : cb - 1;
       half_t* const stg = sB(lastb) + wave * (32 * WN);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = to_f16(acc[i][j][e]);
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              stg[(16 * h + srow + e) * WN + j * 16 + scol] = to_f16(acc[2 * i + h][j][e]);
         const int rbase = m0 + wm * WM + i * 32;
         const int cbase = n0 + wn * OW;
 #pragma unroll
@@ -739,9 +755,11 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) stg[((e >> 2) * 8 + rgrp + (e & 3)) * WN + j * 32 + ccol] = acc[i][j][e];
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * WN + j * 16 + scol] = acc[2 * i + h][j][e];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
       float4 v[PER], res[PER];
@@ -833,12 +851,15 @@ int launch(const GemmParams& p, hipStream_t s) {
   // stages of the current one (no prologue wait, no gap between work-groups).
   // It stages the epilogue in f16 in the slots the last stage frees: f16
   // output, the store and SwiGLU epilogues.
-  // (256 x 256 tiles: the four-wave kernel, with the same rule)
+  // (256 x 256 tiles: the four-wave kernel, whose persistent form also
+  // serves launches of one round, one tile per work-group: its one-tile form,
+  // with the f32 staging of the epilogue, spills registers inside the K loop
+  // on 16 x 16 x 32 products and is kept for f32 output and the residual add)
   const bool persistent = EPI != 1 && p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2;
   if constexpr (BM == 256 && BN == 256) {
     if constexpr (EPI != 1) {
-      if (persistent) {
-        hipLaunchKernelGGL((gemm_f16_w4<EPI, true>), dim3(cus), dim3(256), 0, s, p);
+      if (p.dtype_out == 1 && (cus & 7) == 0 && p.K / kBK >= 2) {
+        hipLaunchKernelGGL((gemm_f16_w4<EPI, true>), dim3(ntiles < cus ? ntiles : cus), dim3(256), 0, s, p);
         return check_launch("gemm");
       }
     }
