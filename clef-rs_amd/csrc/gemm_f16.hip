@@ -1039,7 +1039,9 @@ int gemm_f16_tile_shape(const GemmParams& p, int epilogue, int* bm) {
     return (double)((tiles + cus - 1) / cus) * rows * bn * per_out;
   };
   struct Cand { int bm, bn; double c; };
-  const Cand cands[] = {{256, 256, cost(256, 256, 1.0)},
+  // (the residual epilogue stays off 256 x 256 tiles: the four-wave kernel's
+  // one-tile form, with its f32 staging, spills registers in the K loop)
+  const Cand cands[] = {{256, 256, epilogue == 1 ? 1e300 : cost(256, 256, 1.0)},
                         {256, 192, epilogue == 2 ? 1e300 : cost(256, 192, 1.1)},
                         {256, 128, cost(256, 128, 1.2)},
                         {128, 128, cost(128, 128, 1.5)}};
