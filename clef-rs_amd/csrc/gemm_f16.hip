@@ -742,14 +742,24 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
     vm_wait_all();  // the re-requested stages land before the work-group ends
   } else {
     zero();
-    for (int s = 0; s + 2 < nk; ++s) stage(m0, n0, s + 2, Y_{}, Y_{});
-    if (nk >= 2) stage(0, 0, 0, Y_{}, N_{});
-    stage(0, 0, 0, N_{}, N_{});
+    if (nk >= 2) {
+      // the persistent form's straight-line stage sequence: the last two
+      // stages re-request this tile's first two (in bounds, never read), so
+      // every stage is the same code (with separate tail stages the register
+      // allocator spills inside the K loop); those requests land before the
+      // epilogue reuses their slots
+      for (int s = 0; s + 2 < nk; ++s) stage(m0, n0, s + 2, Y_{}, Y_{});
+      stage(m0, n0, 0, Y_{}, Y_{});
+      stage(m0, n0, 1, Y_{}, Y_{});
+      vm_wait_all();
+    } else {
+      stage(0, 0, 0, N_{}, N_{});
+    }
 
     // epilogue of a one-tile work-group: each wave stages 32 x WN f32 slabs in
     // its own 16 KiB of the tile buffers (the A slots), which the last stage
     // may still be reading for a slower wave: the barrier comes first (no
-    // request is in flight: the last two stages issued none)
+    // request is in flight)
     lds_barrier();
     float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
 #pragma unroll
@@ -852,9 +862,9 @@ int launch(const GemmParams& p, hipStream_t s) {
   // It stages the epilogue in f16 in the slots the last stage frees: f16
   // output, the store and SwiGLU epilogues.
   // (256 x 256 tiles: the four-wave kernel, whose persistent form also
-  // serves launches of one round, one tile per work-group: its one-tile form,
-  // with the f32 staging of the epilogue, spills registers inside the K loop
-  // on 16 x 16 x 32 products and is kept for f32 output and the residual add)
+  // serves launches of one round, one tile per work-group, 1% faster there
+  // than its one-tile form, which stages the epilogue in f32 and serves f32
+  // output and the residual add)
   const bool persistent = EPI != 1 && p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2;
   if constexpr (BM == 256 && BN == 256) {
     if constexpr (EPI != 1) {
@@ -1039,9 +1049,7 @@ int gemm_f16_tile_shape(const GemmParams& p, int epilogue, int* bm) {
     return (double)((tiles + cus - 1) / cus) * rows * bn * per_out;
   };
   struct Cand { int bm, bn; double c; };
-  // (the residual epilogue stays off 256 x 256 tiles: the four-wave kernel's
-  // one-tile form, with its f32 staging, spills registers in the K loop)
-  const Cand cands[] = {{256, 256, epilogue == 1 ? 1e300 : cost(256, 256, 1.0)},
+  const Cand cands[] = {{256, 256, cost(256, 256, 1.0)},
                         {256, 192, epilogue == 2 ? 1e300 : cost(256, 192, 1.1)},
                         {256, 128, cost(256, 128, 1.2)},
                         {128, 128, cost(128, 128, 1.5)}};
