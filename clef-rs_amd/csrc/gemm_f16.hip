@@ -93,6 +93,11 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   constexpr int WM = BM / VM, WN = BN / 2;
   constexpr int TM = WM / 32;                    // 32-row slabs of the epilogue per wave
   constexpr int TM16 = WM / 16, TN16 = WN / 16;  // 16 x 16 product blocks per wave
+  // epilogue staging pitches (f16 and f32 elements): a row 8 halves or 4
+  // floats longer than the wave's columns puts rows 4 apart 16 banks apart,
+  // so the four lane groups of a 16 x 16 accumulator (rows 4 apart, 32 or 64
+  // bytes each) write to disjoint banks
+  constexpr int PWH = WN + 8, PWF = WN + 4;
   constexpr int NA = BM * 8 / 64 / kWaves;  // A DMA instructions per wave per stage
   constexpr int NB = BN * 8 / 64 / kWaves;
   typedef half8 frag;
@@ -104,7 +109,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   auto sA = [&](int st) { return smem + st * kStA; };
   auto sB = [&](int st) { return smem + NSA * kStA + st * kStB; };
   static_assert((NSA == 2 || NSA == 3) && (NSB == NSA || NSB == NSA + 1), "two or three stages per operand");
-  static_assert(kWaves * 32 * WN * 4 <= (int)sizeof(smem), "epilogue staging fits the tile buffers");
+  static_assert(kWaves * 32 * PWF * 4 <= (int)sizeof(smem), "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -337,31 +342,31 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     if constexpr (PERSIST) {
       // ---- epilogue of a persistent work-group.  The next tile's first
       // stages are in flight into the other slots; the slots of this tile's
-      // last stage are free, and each wave stages a 32 x WN slab in f16 there
-      // (waves 0-3 in the A slot, 4-7 in the B slot).  Values are rounded to
-      // f16 once, as the stores would round them (EPI 0), or as SwiGLU rounds
-      // gate and up before combining them (neural.metal:35-42).
-      static_assert(EPI != 1 && kWaves == 8 && 4 * 32 * WN <= kStA && 4 * 32 * WN <= kStB,
+      // last stage are free, and each wave stages 16 x WN slabs in f16 there
+      // (waves 0-3 in the A slot, 4-7 in the B slot; rows PWH apart).  Values
+      // are rounded to f16 once, as the stores would round them (EPI 0), or as
+      // SwiGLU rounds gate and up before combining them (neural.metal:35-42).
+      static_assert(EPI != 1 && kWaves == 8 && 4 * 16 * PWH <= kStA && 4 * 16 * PWH <= kStB,
                     "f16 staging of four waves fits a stage slot");
+      constexpr int PER16 = 16 * CPR / 64;  // chunks per lane per 16-row slab
+      static_assert(16 * CPR % 64 == 0, "whole chunks per lane");
       const int pa = ca == 0 ? NSA - 1 : ca - 1, pb = cb == 0 ? NSB - 1 : cb - 1;
-      half_t* const stg = (wave < 4 ? sA(pa) : sB(pb)) + (wave & 3) * (32 * WN);
+      half_t* const stg = (wave < 4 ? sA(pa) : sB(pb)) + (wave & 3) * (16 * PWH);
       const int scol = lane & 15, srow = (lane >> 4) * 4;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {  // slab i: product block rows 2 i and 2 i + 1
+      for (int i = 0; i < TM16; ++i) {  // slab i: product block row i
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int j = 0; j < TN16; ++j)
 #pragma unroll
-          for (int j = 0; j < TN16; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * WN + j * 16 + scol] = to_f16(acc[2 * i + h][j][e]);
-        const int rbase = m0 + wm * WM + i * 32;
+          for (int e = 0; e < 4; ++e) stg[(srow + e) * PWH + j * 16 + scol] = to_f16(acc[i][j][e]);
+        const int rbase = m0 + wm * WM + i * 16;
         const int cbase = n0 + wn * OW;
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
+        for (int q = 0; q < PER16; ++q) {
           const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
-          half4 h = *reinterpret_cast<const half4*>(stg + row * WN + c4 * 4);
+          half4 h = *reinterpret_cast<const half4*>(stg + row * PWH + c4 * 4);
           if constexpr (EPI == 2) {
-            const half4 u = *reinterpret_cast<const half4*>(stg + row * WN + OW + c4 * 4);
+            const half4 u = *reinterpret_cast<const half4*>(stg + row * PWH + OW + c4 * 4);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               // the same function as clef_silu_mul's (neural.rs:484-492)
@@ -397,7 +402,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
     // and read back as 4-column chunks, so the global accesses are 8- or
     // 16-byte vectors along the rows.  (LDS operations of one wave complete
     // in order, so the write -> read -> next write sequence needs no barrier.)
-    float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
+    float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * PWF);
     const int scol = lane & 15, srow = (lane >> 4) * 4;
   #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -406,7 +411,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   #pragma unroll
         for (int j = 0; j < TN16; ++j)
   #pragma unroll
-          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * WN + j * 16 + scol] = acc[2 * i + h][j][e];
+          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * PWF + j * 16 + scol] = acc[2 * i + h][j][e];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
       float4 v[PER], res[PER];
@@ -414,8 +419,8 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       for (int q = 0; q < PER; ++q) {
         const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
         if (EPI == 2) {
-          const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
-          const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
+          const float4 g = *reinterpret_cast<const float4*>(stg + row * PWF + c4 * 4);
+          const float4 u = *reinterpret_cast<const float4*>(stg + row * PWF + OW + c4 * 4);
           // half roundings of neural.metal:35-42; SiLU on the hardware exp2 and
           // reciprocal (expf and an IEEE division cost ~1.8% of a prefill
           // here), the same function as clef_silu_mul's, so fused and unfused
@@ -427,7 +432,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
           };
           v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
         } else {
-          v[q] = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+          v[q] = *reinterpret_cast<const float4*>(stg + row * PWF + c4 * 4);
         }
       }
       if (EPI == 1) {
@@ -512,8 +517,10 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) half_t smem[2 * kStA + 3 * kStB];
   auto sA = [&](int st) { return smem + st * kStA; };
   auto sB = [&](int st) { return smem + 2 * kStA + st * kStB; };
-  static_assert(kWaves * 32 * WN * 4 <= (int)sizeof(smem), "one-tile epilogue staging fits");
-  static_assert(kWaves * 32 * WN * 2 <= kStB * 2, "persistent epilogue staging fits one B slot");
+  // epilogue staging pitches, as gemm_f16_dma's (rows 4 apart 16 banks apart)
+  constexpr int PWH = WN + 8, PWF = WN + 4;
+  static_assert(kWaves * 32 * PWF * 4 <= (int)sizeof(smem), "one-tile epilogue staging fits");
+  static_assert(kWaves * 16 * PWH <= kStB, "persistent epilogue staging fits one B slot");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -689,29 +696,27 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 
       // epilogue: the B slot of this tile's last stage is free (every wave
       // passed that stage's barrier, and the next request into it is the
-      // next tile's B(2)); each wave stages its 32 x WN slabs there in f16,
-      // rounded once as the stores would be, and as SwiGLU rounds gate and
-      // up before combining them (neural.metal:35-42).  Slab i holds the
-      // 16-row blocks 2 i and 2 i + 1.
+      // next tile's B(2)); each wave stages its 16 x WN slabs there in f16
+      // (rows PWH apart), rounded once as the stores would be, and as SwiGLU
+      // rounds gate and up before combining them (neural.metal:35-42).  Slab
+      // i holds the 16-row block i.
+      constexpr int PER16 = 16 * CPR / 64;  // chunks per lane per slab
       const int lastb = cb == 0 ? 2 : cb - 1;
-      half_t* const stg = sB(lastb) + wave * (32 * WN);
+      half_t* const stg = sB(lastb) + wave * (16 * PWH);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
+      for (int i = 0; i < 8; ++i) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int j = 0; j < 8; ++j)
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              stg[(16 * h + srow + e) * WN + j * 16 + scol] = to_f16(acc[2 * i + h][j][e]);
-        const int rbase = m0 + wm * WM + i * 32;
+          for (int e = 0; e < 4; ++e) stg[(srow + e) * PWH + j * 16 + scol] = to_f16(acc[i][j][e]);
+        const int rbase = m0 + wm * WM + i * 16;
         const int cbase = n0 + wn * OW;
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
+        for (int q = 0; q < PER16; ++q) {
           const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
-          half4 h = *reinterpret_cast<const half4*>(stg + row * WN + c4 * 4);
+          half4 h = *reinterpret_cast<const half4*>(stg + row * PWH + c4 * 4);
           if constexpr (EPI == 2) {
-            const half4 u = *reinterpret_cast<const half4*>(stg + row * WN + OW + c4 * 4);
+            const half4 u = *reinterpret_cast<const half4*>(stg + row * PWH + OW + c4 * 4);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               // the same function as clef_silu_mul's (neural.rs:484-492)
@@ -756,12 +761,12 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       stage(0, 0, 0, N_{}, N_{});
     }
 
-    // epilogue of a one-tile work-group: each wave stages 32 x WN f32 slabs in
-    // its own 16 KiB of the tile buffers (the A slots), which the last stage
-    // may still be reading for a slower wave: the barrier comes first (no
-    // request is in flight)
+    // epilogue of a one-tile work-group: each wave stages 32 x WN f32 slabs
+    // (rows PWF apart) in its own 16.5 KiB of the tile buffers, which the
+    // last stage may still be reading for a slower wave: the barrier comes
+    // first (no request is in flight)
     lds_barrier();
-    float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * WN);
+    float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * PWF);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -769,7 +774,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * WN + j * 16 + scol] = acc[2 * i + h][j][e];
+          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * PWF + j * 16 + scol] = acc[2 * i + h][j][e];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
       float4 v[PER], res[PER];
@@ -777,8 +782,8 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       for (int q = 0; q < PER; ++q) {
         const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
         if (EPI == 2) {
-          const float4 g = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
-          const float4 u = *reinterpret_cast<const float4*>(stg + row * WN + OW + c4 * 4);
+          const float4 g = *reinterpret_cast<const float4*>(stg + row * PWF + c4 * 4);
+          const float4 u = *reinterpret_cast<const float4*>(stg + row * PWF + OW + c4 * 4);
           auto sw = [](float gv, float uv) {  // as gemm_f16_dma's (neural.metal:35-42)
             const float gh = static_cast<float>(to_f16(gv));
             const float sh = static_cast<float>(to_f16(silu_hw(gh)));
@@ -786,7 +791,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
           };
           v[q] = make_float4(sw(g.x, u.x), sw(g.y, u.y), sw(g.z, u.z), sw(g.w, u.w));
         } else {
-          v[q] = *reinterpret_cast<const float4*>(stg + row * WN + c4 * 4);
+          v[q] = *reinterpret_cast<const float4*>(stg + row * PWF + c4 * 4);
         }
       }
       if (EPI == 1) {  // residual reads all issued before the first store
