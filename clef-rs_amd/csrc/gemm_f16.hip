@@ -668,6 +668,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 
   const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
   const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
+  const bool yvec8 = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * 2)) & 15) == 0;  // f16 rows
   constexpr int OW = EPI == 2 ? WN / 2 : WN;  // output columns per wave
   constexpr int CPR = OW / 4, PER = 32 * CPR / 64;
   const int scol = lane & 15, srow = (lane >> 4) * 4;
@@ -700,7 +701,9 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       // (rows PWH apart), rounded once as the stores would be, and as SwiGLU
       // rounds gate and up before combining them (neural.metal:35-42).  Slab
       // i holds the 16-row block i.
-      constexpr int PER16 = 16 * CPR / 64;  // chunks per lane per slab
+      // read back as 8-column chunks (16-byte loads and stores)
+      constexpr int CPR8 = OW / 8, PER8 = 16 * CPR8 / 64;  // chunks per row, per lane per slab
+      static_assert(16 * CPR8 % 64 == 0, "whole chunks per lane");
       const int lastb = cb == 0 ? 2 : cb - 1;
       half_t* const stg = sB(lastb) + wave * (16 * PWH);
 #pragma unroll
@@ -712,26 +715,26 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
         const int rbase = m0 + wm * WM + i * 16;
         const int cbase = n0 + wn * OW;
 #pragma unroll
-        for (int q = 0; q < PER16; ++q) {
-          const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
-          half4 h = *reinterpret_cast<const half4*>(stg + row * PWH + c4 * 4);
+        for (int q = 0; q < PER8; ++q) {
+          const int idx = q * 64 + lane, row = idx / CPR8, c8 = idx % CPR8;
+          half8 h = *reinterpret_cast<const half8*>(stg + row * PWH + c8 * 8);
           if constexpr (EPI == 2) {
-            const half4 u = *reinterpret_cast<const half4*>(stg + row * PWH + OW + c4 * 4);
+            const half8 u = *reinterpret_cast<const half8*>(stg + row * PWH + OW + c8 * 8);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int t = 0; t < 8; ++t) {
               // the same function as clef_silu_mul's (neural.rs:484-492)
               const float sh = static_cast<float>(to_f16(silu_hw(static_cast<float>(h[t]))));
               h[t] = static_cast<half_t>(sh * static_cast<float>(u[t]));
             }
           }
-          const int r = rbase + row, c = cbase + c4 * 4;
+          const int r = rbase + row, c = cbase + c8 * 8;
           if (r >= p.M) continue;
           half_t* dst = static_cast<half_t*>(p.y) + (int64_t)r * p.ldy + c;
-          if (yvec && c + 3 < p.N) {
-            *reinterpret_cast<half4*>(dst) = h;
+          if (yvec8 && c + 7 < p.N) {
+            *reinterpret_cast<half8*>(dst) = h;
           } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+            for (int t = 0; t < 8; ++t)
               if (c + t < p.N) dst[t] = h[t];
           }
         }
