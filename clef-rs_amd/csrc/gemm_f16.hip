@@ -266,6 +266,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   static_assert(!PF || NR % kPD == 0, "prefetch batches");
   const int esz = (EPI == 1 || p.dtype_out != 1) ? 4 : 2;
   const bool yvec = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * esz)) & (4 * esz - 1)) == 0;
+  const bool yvec8 = ((reinterpret_cast<uintptr_t>(p.y) | (uintptr_t)(p.ldy * 2)) & 15) == 0;  // f16 rows
   float4 pre[PF ? NR : 1];
   auto prefetch = [&](int b) {
 #pragma unroll
@@ -348,8 +349,9 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       // SwiGLU rounds gate and up before combining them (neural.metal:35-42).
       static_assert(EPI != 1 && kWaves == 8 && 4 * 16 * PWH <= kStA && 4 * 16 * PWH <= kStB,
                     "f16 staging of four waves fits a stage slot");
-      constexpr int PER16 = 16 * CPR / 64;  // chunks per lane per 16-row slab
-      static_assert(16 * CPR % 64 == 0, "whole chunks per lane");
+      // read back as 8-column chunks (16-byte loads and stores)
+      constexpr int CPR8 = OW / 8, PER8 = 16 * CPR8 / 64;  // chunks per row, per lane per slab
+      static_assert(16 * CPR8 % 64 == 0, "whole chunks per lane");
       const int pa = ca == 0 ? NSA - 1 : ca - 1, pb = cb == 0 ? NSB - 1 : cb - 1;
       half_t* const stg = (wave < 4 ? sA(pa) : sB(pb)) + (wave & 3) * (16 * PWH);
       const int scol = lane & 15, srow = (lane >> 4) * 4;
@@ -362,26 +364,26 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
         const int rbase = m0 + wm * WM + i * 16;
         const int cbase = n0 + wn * OW;
 #pragma unroll
-        for (int q = 0; q < PER16; ++q) {
-          const int idx = q * 64 + lane, row = idx / CPR, c4 = idx % CPR;
-          half4 h = *reinterpret_cast<const half4*>(stg + row * PWH + c4 * 4);
+        for (int q = 0; q < PER8; ++q) {
+          const int idx = q * 64 + lane, row = idx / CPR8, c8 = idx % CPR8;
+          half8 h = *reinterpret_cast<const half8*>(stg + row * PWH + c8 * 8);
           if constexpr (EPI == 2) {
-            const half4 u = *reinterpret_cast<const half4*>(stg + row * PWH + OW + c4 * 4);
+            const half8 u = *reinterpret_cast<const half8*>(stg + row * PWH + OW + c8 * 8);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int t = 0; t < 8; ++t) {
               // the same function as clef_silu_mul's (neural.rs:484-492)
               const float sh = static_cast<float>(to_f16(silu_hw(static_cast<float>(h[t]))));
               h[t] = static_cast<half_t>(sh * static_cast<float>(u[t]));
             }
           }
-          const int r = rbase + row, c = cbase + c4 * 4;
+          const int r = rbase + row, c = cbase + c8 * 8;
           if (r >= p.M) continue;
           half_t* dst = static_cast<half_t*>(p.y) + (int64_t)r * p.ldy + c;
-          if (yvec && c + 3 < p.N) {
-            *reinterpret_cast<half4*>(dst) = h;
+          if (yvec8 && c + 7 < p.N) {
+            *reinterpret_cast<half8*>(dst) = h;
           } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+            for (int t = 0; t < 8; ++t)
               if (c + t < p.N) dst[t] = h[t];
           }
         }
@@ -414,6 +416,43 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
           for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * PWF + j * 16 + scol] = acc[2 * i + h][j][e];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
+      if constexpr (EPI != 1) {
+        if (esz == 2) {  // f16 output: 8-column chunks, 16-byte stores
+          constexpr int CPR8 = OW / 8, PER8 = 32 * CPR8 / 64;
+          static_assert(32 * CPR8 % 64 == 0, "whole chunks per lane");
+  #pragma unroll
+          for (int q = 0; q < PER8; ++q) {
+            const int idx = q * 64 + lane, row = idx / CPR8, c8 = idx % CPR8;
+            const float* src = stg + row * PWF + c8 * 8;
+            float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+            if constexpr (EPI == 2) {
+              const float4 ulo = *reinterpret_cast<const float4*>(src + OW);
+              const float4 uhi = *reinterpret_cast<const float4*>(src + OW + 4);
+              auto sw = [](float gv, float uv) {  // as below (neural.metal:35-42)
+                const float gh = static_cast<float>(to_f16(gv));
+                const float sh = static_cast<float>(to_f16(silu_hw(gh)));
+                return sh * static_cast<float>(to_f16(uv));
+              };
+              lo = make_float4(sw(lo.x, ulo.x), sw(lo.y, ulo.y), sw(lo.z, ulo.z), sw(lo.w, ulo.w));
+              hi = make_float4(sw(hi.x, uhi.x), sw(hi.y, uhi.y), sw(hi.z, uhi.z), sw(hi.w, uhi.w));
+            }
+            const int r = rbase + row, c = cbase + c8 * 8;
+            if (r >= p.M) continue;
+            const half8 h = {static_cast<half_t>(lo.x), static_cast<half_t>(lo.y), static_cast<half_t>(lo.z),
+                             static_cast<half_t>(lo.w), static_cast<half_t>(hi.x), static_cast<half_t>(hi.y),
+                             static_cast<half_t>(hi.z), static_cast<half_t>(hi.w)};
+            half_t* dst = static_cast<half_t*>(p.y) + (int64_t)r * p.ldy + c;
+            if (yvec8 && c + 7 < p.N) {
+              *reinterpret_cast<half8*>(dst) = h;
+            } else {
+  #pragma unroll
+              for (int t = 0; t < 8; ++t)
+                if (c + t < p.N) dst[t] = h[t];
+            }
+          }
+          continue;
+        }
+      }
       float4 v[PER], res[PER];
   #pragma unroll
       for (int q = 0; q < PER; ++q) {
