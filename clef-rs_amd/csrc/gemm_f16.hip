@@ -665,6 +665,15 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   // has1 / has2: stages s+1 / s+2 exist (compile-time, so the steady state
   // has no branches between its instructions); the stage-(s+2) requests go
   // to tile (tm2, tn2) at k-stage ks2.
+  // A persistent tile's epilogue issues its global stores after the requests
+  // of the next tile's first two stages and before that tile's B(2): when the
+  // tile was whole (epi_pending), exactly SEPI stores per wave, so the first
+  // stage's wait can leave them in flight (vmcnt counts in issue order).
+  // Store epilogue only: with SwiGLU's the flag made the compiler peel the
+  // first stage, which spilled registers.
+  constexpr int SEPI = 8 * (16 * ((EPI == 2 ? WN / 2 : WN) / 8) / 64);
+  static_assert(NB + SEPI < 64, "vmcnt is 6 bits");
+  bool epi_pending = false;
   int ca = 0, cb = 0;
   auto stage = [&](int tm2, int tn2, int ks2, auto has1_t, auto has2_t) {
     constexpr bool has1 = decltype(has1_t)::value, has2 = decltype(has2_t)::value;
@@ -683,11 +692,16 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
           if (m >= 17 && m < 49 && ((m - 17) & 3) == 0 && has2) dma_b(nb2, tn2, ks2, (m - 17) >> 2);
         } else {
           if (m == 6 && has1) {
-            // in flight after stage s+1's requests: B(s+2) only
-            if (has2)
-              vm_wait<NB>();
-            else
+            // in flight after stage s+1's requests: B(s+2) only, and in the
+            // first stage after a whole tile's epilogue, its stores
+            if (has2) {
+              if (EPI == 0 && epi_pending)
+                vm_wait<NB + SEPI>();
+              else
+                vm_wait<NB>();
+            } else {
               vm_wait_all();
+            }
             lds_barrier();
           }
           if (has1) {
@@ -701,6 +715,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
     }
     ca = ca1;
     cb = cb1;
+    epi_pending = false;
   };
   typedef std::true_type Y_;
   typedef std::false_type N_;
@@ -745,6 +760,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       static_assert(16 * CPR8 % 64 == 0, "whole chunks per lane");
       const int lastb = cb == 0 ? 2 : cb - 1;
       half_t* const stg = sB(lastb) + wave * (16 * PWH);
+      const bool whole = yvec8 && m0 + BM <= p.M && n0 + (EPI == 2 ? BN / 2 : BN) <= p.N;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
@@ -767,17 +783,22 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
             }
           }
           const int r = rbase + row, c = cbase + c8 * 8;
-          if (r >= p.M) continue;
           half_t* dst = static_cast<half_t*>(p.y) + (int64_t)r * p.ldy + c;
-          if (yvec8 && c + 7 < p.N) {
+          if (whole) {  // one 16-byte store per chunk: SEPI per wave
             *reinterpret_cast<half8*>(dst) = h;
           } else {
+            if (r >= p.M) continue;
+            if (yvec8 && c + 7 < p.N) {
+              *reinterpret_cast<half8*>(dst) = h;
+            } else {
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
-              if (c + t < p.N) dst[t] = h[t];
+              for (int t = 0; t < 8; ++t)
+                if (c + t < p.N) dst[t] = h[t];
+            }
           }
         }
       }
+      epi_pending = EPI == 0 && whole;
       if (!next) break;
       // every wave's staging reads are done before the next tile's first
       // stage requests B(2) into this slot
