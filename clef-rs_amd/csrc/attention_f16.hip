@@ -829,7 +829,46 @@ __global__ __launch_bounds__(512) void attn_f16_w8(AttnParams p) {
     }
     return r;
   };
-  if (p.vec_io) {
+  if (p.vec_io == 2) {
+    // 16-byte gate and output rows: round(O / l) of the wave's 16 queries is
+    // staged in LDS (free after the last key tile; waves 0-3 in sK, 4-7 in
+    // sV; rows PWS halves apart, so the 8-byte writes of a lane half cover
+    // the 64 banks once), then each lane takes 8 consecutive d of one query:
+    // 16-byte gate loads (issued once O is staged) and stores of whole row
+    // pieces
+    constexpr int PWS = D + 8, CH = D / 8, RPI = 64 / CH, NR = 16 / RPI;
+    static_assert(4 * 16 * PWS <= 2 * BK * D, "four waves' staging fits sK or sV");
+    half_t* const stg = (wave < 4 ? &sK[0][0] : &sV[0][0]) + (wave & 3) * (16 * PWS);
+    const int c8 = 8 * (lane % CH), rl = lane / CH;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      half4 a4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a4[e] = to_f16(O[t][e] * inv);
+      *reinterpret_cast<half4*>(stg + n * PWS + 16 * t + 4 * g) = a4;
+    }
+    half8 gv[NR];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      const int rq = q0 + 16 * wave + RPI * q + rl;
+      const int64_t pr = qb0 + min(rq, qn - 1);
+      gv[q] = *reinterpret_cast<const half8*>(static_cast<const half_t*>(p.gate) + pr * p.ldg + (int64_t)h * p.hsg + c8);
+    }
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      const int rr = RPI * q + rl, rq = q0 + 16 * wave + rr;
+      const half8 av = *reinterpret_cast<const half8*>(stg + rr * PWS + c8);
+      half8 r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sg = static_cast<float>(to_f16(sigmoid_hw(static_cast<float>(gv[q][e]))));
+        r[e] = static_cast<half_t>(static_cast<float>(av[e]) * sg);
+      }
+      if (rq < qn)
+        *reinterpret_cast<half8*>(static_cast<half_t*>(p.y) + (int64_t)(qb0 + rq) * p.ldy + (int64_t)h * d + c8) = r;
+    }
+    lds_barrier();  // staging reads done before the next item's DMA refills sK / sV
+  } else if (p.vec_io) {
     half4 gv[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
@@ -924,6 +963,10 @@ int launch_w8(const AttnParams& p0, hipStream_t s) {
   AttnParams p = p0;
   p.vec_io = ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.y)) & 7) == 0 &&
              p.ldg % 4 == 0 && p.hsg % 4 == 0 && p.ldy % 4 == 0 && p.d % 4 == 0;
+  // 16-byte gate and output rows (the staged epilogue): a full head width
+  if (p.vec_io && ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.y)) & 15) == 0 &&
+      p.ldg % 8 == 0 && p.hsg % 8 == 0 && p.ldy % 8 == 0 && p.d == D)
+    p.vec_io = 2;
   // resident work-groups (CUs x occupancy) of the instance launched, per
   // device: the ragged instance carries the prefix-segment logic and may fit
   // fewer per CU, and a grid above the resident count would lose the
