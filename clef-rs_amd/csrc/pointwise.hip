@@ -612,18 +612,24 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
                                                           int64_t ldy_tok, int heads, int rot, int pos0,
                                                           int dst_offset, float eps, float inv_width, int vec,
                                                           RotaryTable tab, const int* __restrict__ cu, int nseq,
-                                                          float2* __restrict__ tab_out) {
+                                                          float2* __restrict__ tab_out, int T) {
   constexpr int D = 64 * EPL;
-  __shared__ float cs[128], sn[128];
-  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // one token per wave (four per work-group): its angles, then all its heads
+  __shared__ float cs_all[4][128], sn_all[4][128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = 4 * blockIdx.x + wave;
+  if (t >= T) return;  // whole waves; no barrier below
+  float* const cs = cs_all[wave];
+  float* const sn = sn_all[wave];
   const int half = rot / 2;
   // position: pos0 + t, or pos0 + (t - first token of t's sequence)
   const float p = static_cast<float>(pos0 + (cu ? t - seq_start(cu, nseq, t) : t));
-  for (int f = threadIdx.x; f < half; f += 256) {
+  for (int f = lane; f < half; f += 64) {
     rotary_angle(p, tab.inv_freq[f], cs[f], sn[f]);
     if (tab_out) tab_out[(int64_t)t * half + f] = make_float2(cs[f], sn[f]);
   }
-  __syncthreads();
+  // the wave's own LDS writes complete before its reads below (in order)
+  __builtin_amdgcn_wave_barrier();
   const int i0 = lane * EPL;
   const int pd = half / EPL;  // partner lane distance
   float wv[EPL], cw[EPL], sw[EPL];
@@ -635,7 +641,7 @@ __global__ __launch_bounds__(256) void qk_norm_rotary_tok(const TI* __restrict__
     cw[e] = i < rot ? cs[f] : 1.0f;
     sw[e] = i < rot ? (i < half ? -sn[f] : sn[f]) : 0.0f;  // r = -v[i + half] below half, v[i - half] above
   }
-  for (int h = wave; h < heads; h += 4) {
+  for (int h = 0; h < heads; ++h) {
     const TI* src = x + (int64_t)t * ldx + (int64_t)h * hs + i0;
     float v[EPL];
     bool got = false;
@@ -998,9 +1004,9 @@ static bool qk_norm_rotary_tok_launch(const void* x, int64_t ldx, int64_t hs, in
                       : 0;
   const float inv = static_cast<float>(1.0 / static_cast<double>(d));
 #define CLEF_QKR(E, TI, TO)                                                                                     \
-  hipLaunchKernelGGL((qk_norm_rotary_tok<E, TI, TO>), dim3(T), dim3(256), 0, st, static_cast<const TI*>(x), ldx, \
-                     hs, w, static_cast<TO*>(y), ldy_tok, heads, rot, pos0, dst_offset, eps, inv, vec, tab, cu, nseq, \
-                     tab_out)
+  hipLaunchKernelGGL((qk_norm_rotary_tok<E, TI, TO>), dim3((T + 3) / 4), dim3(256), 0, st,                     \
+                     static_cast<const TI*>(x), ldx, hs, w, static_cast<TO*>(y), ldy_tok, heads, rot, pos0, dst_offset, \
+                     eps, inv, vec, tab, cu, nseq, tab_out, T)
 #define CLEF_QKR_E(TI, TO)      \
   if (epl == 4)                 \
     CLEF_QKR(4, TI, TO);        \
