@@ -544,13 +544,15 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
 // cores idle while both waves of a SIMD wait on LDS.  Same rings (A: 2
 // stages, B: 3), swizzle, tile order, products and epilogue arithmetic as
 // gemm_f16_dma, so results are bit-identical to it.
-template <int EPI, bool PERSIST>
+template <int EPI, bool PERSIST, int BN>
 __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
-  constexpr int BM = 256, BN = 256, VM = 2;
+  constexpr int BM = 256, VM = 2;
   constexpr int kWaves = VM * 2;
-  constexpr int WM = BM / VM, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-  constexpr int NA = BM * 8 / 64 / kWaves, NB = BN * 8 / 64 / kWaves;  // 8 DMA instructions each
-  static_assert(TM == 4 && TN == 4 && NA == 8 && NB == 8, "the hand schedule below assumes 128 x 128 per wave");
+  constexpr int WM = BM / VM, WN = BN / 2, TM = WM / 32;
+  constexpr int TN16 = WN / 16;                                         // 16-column blocks per wave
+  constexpr int NA = BM * 8 / 64 / kWaves, NB = BN * 8 / 64 / kWaves;  // DMA instructions per stage
+  static_assert(TM == 4 && NA == 8 && ((BN == 256 && NB == 8) || (BN == 128 && NB == 4)),
+                "the hand schedules below assume 128 x 128 or 128 x 64 per wave");
   typedef half8 frag;
   constexpr int kStA = BM * kBK, kStB = BN * kBK;
   __shared__ __attribute__((aligned(1024))) half_t smem[2 * kStA + 3 * kStB];
@@ -621,7 +623,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   int goff[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) goff[ks] = 2 * (r16 * kBK + (((4 * ks + c16) ^ ((r16 >> 1) & 7)) << 3));
-  frag FA[8], FB[2][8];
+  frag FA[8], FB[2][TN16];
   auto rd = [&](int sa, int sb, int ks, int q, int fb) {  // q < 8: A block q, else B block q - 8 into FB[fb]
     if (q < 8)
       FA[q] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sA(sa)) + wm * WM * kBK * 2 + goff[ks] +
@@ -631,7 +633,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
                                                      goff[ks] + (q - 8) * 16 * kBK * 2);
   };
   // acc[I][J] holds rows 16 I + 4 (lane / 16) + e, column 16 J + lane % 16
-  float4_t acc[8][8];
+  float4_t acc[8][TN16];
 
   const int nk = p.K / kBK;
   // prologue: stages 0 and 1 requested, stage 0 published, its first k-block
@@ -652,16 +654,19 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   }
   lds_barrier();
 #pragma unroll
-  for (int q = 0; q < 16; ++q) rd(0, 0, 0, q, 0);
+  for (int q = 0; q < 8 + TN16; ++q) rd(0, 0, 0, q, 0);
 
-  // One stage: 2 k-steps x 64 products (block row I outer, column J inner).
-  // In k-step 0 the products carry k-step 1's fragment reads (B during the
-  // first 16, A block I after its last product) and, from product 17, the
-  // DMA of B two stages ahead (into the slot stage s-1 freed), one per four.
-  // In k-step 1 the wave waits at product 6 for its own requests of stage
-  // s+1, the barrier publishes them and frees stage s's A slot, and the
-  // products carry stage s+1's first fragment reads and, from product 9, the
-  // DMA of A two stages ahead.
+  // One stage: 2 k-steps x P products (P = 8 TN16; block row I outer, column
+  // J inner).  In k-step 0 the products carry k-step 1's fragment reads (B
+  // one per two products from product 1, A block I after its last product)
+  // and, from product P/4 + 1, the DMA of B two stages ahead (into the slot
+  // stage s-1 freed), one per four products.  In k-step 1 the wave waits at
+  // product P/8 - 2 (6 or 2) for its own requests of stage s+1, the barrier
+  // publishes them and frees stage s's A slot, and the products carry stage
+  // s+1's first fragment reads and the DMA of A two stages ahead (128 x 128
+  // per wave: B reads at the odd products 9 .. 23, A requests one per four
+  // from product 9; 128 x 64: B reads at the even products 4 .. 10, A
+  // requests one per three from product 5).
   // has1 / has2: stages s+1 / s+2 exist (compile-time, so the steady state
   // has no branches between its instructions); the stage-(s+2) requests go
   // to tile (tm2, tn2) at k-stage ks2.
@@ -671,6 +676,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   // stage's wait can leave them in flight (vmcnt counts in issue order).
   // Store epilogue only: with SwiGLU's the flag made the compiler peel the
   // first stage, which spilled registers.
+  constexpr int P = 8 * TN16;
   constexpr int SEPI = 8 * (16 * ((EPI == 2 ? WN / 2 : WN) / 8) / 64);
   static_assert(NB + SEPI < 64, "vmcnt is 6 bits");
   bool epi_pending = false;
@@ -682,16 +688,17 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int m = 0; m < 64; ++m) {
-        const int I = m >> 3, J = m & 7;
+      for (int m = 0; m < P; ++m) {
+        const int I = m / TN16, J = m % TN16;
         acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(FA[I], FB[ks][J], acc[I][J], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         if (ks == 0) {
-          if ((m & 7) == 7) rd(ca, cb, 1, I, 0);
-          if (m < 16 && (m & 1)) rd(ca, cb, 1, 8 + (m >> 1), 1);
-          if (m >= 17 && m < 49 && ((m - 17) & 3) == 0 && has2) dma_b(nb2, tn2, ks2, (m - 17) >> 2);
+          if (J == TN16 - 1) rd(ca, cb, 1, I, 0);
+          if (m < 2 * TN16 && (m & 1)) rd(ca, cb, 1, 8 + (m >> 1), 1);
+          if (m > P / 4 && m <= P / 4 + 4 * NB && ((m - P / 4 - 1) & 3) == 0 && has2)
+            dma_b(nb2, tn2, ks2, (m - P / 4 - 1) >> 2);
         } else {
-          if (m == 6 && has1) {
+          if (m == P / 8 - 2 && has1) {
             // in flight after stage s+1's requests: B(s+2) only, and in the
             // first stage after a whole tile's epilogue, its stores
             if (has2) {
@@ -705,9 +712,14 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
             lds_barrier();
           }
           if (has1) {
-            if ((m & 7) == 7) rd(ca1, cb1, 0, I, 0);
-            if (m >= 8 && m < 24 && (m & 1)) rd(ca1, cb1, 0, 8 + ((m - 8) >> 1), 0);
-            if (m >= 9 && m < 41 && ((m - 9) & 3) == 0 && has2) dma_a(na2, tm2, ks2, (m - 9) >> 2);
+            if (J == TN16 - 1) rd(ca1, cb1, 0, I, 0);
+            if constexpr (BN == 256) {
+              if (m >= 8 && m < 24 && (m & 1)) rd(ca1, cb1, 0, 8 + ((m - 8) >> 1), 0);
+              if (m >= 9 && m < 41 && ((m - 9) & 3) == 0 && has2) dma_a(na2, tm2, ks2, (m - 9) >> 2);
+            } else {
+              if (m >= 4 && m < 12 && !(m & 1)) rd(ca1, cb1, 0, 8 + ((m - 4) >> 1), 0);
+              if (m >= 5 && m < 29 && (m - 5) % 3 == 0 && has2) dma_a(na2, tm2, ks2, (m - 5) / 3);
+            }
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -730,7 +742,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < TN16; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   };
 
   if constexpr (PERSIST) {
@@ -764,7 +776,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < TN16; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e) stg[(srow + e) * PWH + j * 16 + scol] = to_f16(acc[i][j][e]);
         const int rbase = m0 + wm * WM + i * 16;
@@ -835,7 +847,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < TN16; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * PWF + j * 16 + scol] = acc[2 * i + h][j][e];
       const int rbase = m0 + wm * WM + i * 32;
@@ -934,14 +946,14 @@ int launch(const GemmParams& p, hipStream_t s) {
   // than its one-tile form, which stages the epilogue in f32 and serves f32
   // output and the residual add)
   const bool persistent = EPI != 1 && p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2;
-  if constexpr (BM == 256 && BN == 256) {
+  if constexpr (BM == 256 && (BN == 256 || (BN == 128 && EPI != 1))) {
     if constexpr (EPI != 1) {
       if (p.dtype_out == 1 && (cus & 7) == 0 && p.K / kBK >= 2) {
-        hipLaunchKernelGGL((gemm_f16_w4<EPI, true>), dim3(ntiles < cus ? ntiles : cus), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((gemm_f16_w4<EPI, true, BN>), dim3(ntiles < cus ? ntiles : cus), dim3(256), 0, s, p);
         return check_launch("gemm");
       }
     }
-    hipLaunchKernelGGL((gemm_f16_w4<EPI, false>), dim3(ntiles), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_f16_w4<EPI, false, BN>), dim3(ntiles), dim3(256), 0, s, p);
   } else {
     if constexpr (EPI != 1) {
       if (persistent) {
