@@ -551,8 +551,8 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   constexpr int WM = BM / VM, WN = BN / 2, TM = WM / 32;
   constexpr int TN16 = WN / 16;                                         // 16-column blocks per wave
   constexpr int NA = BM * 8 / 64 / kWaves, NB = BN * 8 / 64 / kWaves;  // DMA instructions per stage
-  static_assert(TM == 4 && NA == 8 && ((BN == 256 && NB == 8) || (BN == 128 && NB == 4)),
-                "the hand schedules below assume 128 x 128 or 128 x 64 per wave");
+  static_assert(TM == 4 && NA == 8 && ((BN == 256 && NB == 8) || (BN == 192 && NB == 6) || (BN == 128 && NB == 4)),
+                "the hand schedules below assume 128 x 128, 128 x 96 or 128 x 64 per wave");
   typedef half8 frag;
   constexpr int kStA = BM * kBK, kStB = BN * kBK;
   __shared__ __attribute__((aligned(1024))) half_t smem[2 * kStA + 3 * kStB];
@@ -665,8 +665,8 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
   // publishes them and frees stage s's A slot, and the products carry stage
   // s+1's first fragment reads and the DMA of A two stages ahead (128 x 128
   // per wave: B reads at the odd products 9 .. 23, A requests one per four
-  // from product 9; 128 x 64: B reads at the even products 4 .. 10, A
-  // requests one per three from product 5).
+  // from product 9; 128 x 96 and 128 x 64: B reads at the even products
+  // from 4, A requests one per three from product 5).
   // has1 / has2: stages s+1 / s+2 exist (compile-time, so the steady state
   // has no branches between its instructions); the stage-(s+2) requests go
   // to tile (tm2, tn2) at k-stage ks2.
@@ -717,7 +717,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
               if (m >= 8 && m < 24 && (m & 1)) rd(ca1, cb1, 0, 8 + ((m - 8) >> 1), 0);
               if (m >= 9 && m < 41 && ((m - 9) & 3) == 0 && has2) dma_a(na2, tm2, ks2, (m - 9) >> 2);
             } else {
-              if (m >= 4 && m < 12 && !(m & 1)) rd(ca1, cb1, 0, 8 + ((m - 4) >> 1), 0);
+              if (m >= 4 && m < 4 + 2 * TN16 && !(m & 1)) rd(ca1, cb1, 0, 8 + ((m - 4) >> 1), 0);
               if (m >= 5 && m < 29 && (m - 5) % 3 == 0 && has2) dma_a(na2, tm2, ks2, (m - 5) / 3);
             }
           }
@@ -946,7 +946,7 @@ int launch(const GemmParams& p, hipStream_t s) {
   // than its one-tile form, which stages the epilogue in f32 and serves f32
   // output and the residual add)
   const bool persistent = EPI != 1 && p.dtype_out == 1 && ntiles > cus && (cus & 7) == 0 && p.K / kBK >= 2;
-  if constexpr (BM == 256 && (BN == 256 || (BN == 128 && EPI != 1))) {
+  if constexpr (BM == 256 && (BN == 256 || (BN != 256 && EPI != 1))) {
     if constexpr (EPI != 1) {
       if (p.dtype_out == 1 && (cus & 7) == 0 && p.K / kBK >= 2) {
         hipLaunchKernelGGL((gemm_f16_w4<EPI, true, BN>), dim3(ntiles < cus ? ntiles : cus), dim3(256), 0, s, p);
