@@ -178,8 +178,9 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
   };
 
   // Products on v_mfma_f32_16x16x32_f16 (the four-wave kernel's, so both
-  // kernels sum every output in the same order): acc[I][J] holds rows
-  // 16 I + 4 (lane / 16) + e, column 16 J + lane % 16 of the wave's block.
+  // kernels sum every output in the same order), weights as the A operand:
+  // acc[I][J] holds row 16 I + lane % 16, columns 16 J + 4 (lane / 16) + e of
+  // the wave's block, so a lane's four results stage as one LDS write.
   float4_t acc[TM16][TN16];
 
   // fragment reads: row r = (wave offset) + 16 i + lane % 16, 16-byte chunk
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       for (int i = 0; i < TM16; ++i)
 #pragma unroll
         for (int j = 0; j < TN16; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[ks][j], af[ks][i], acc[i][j], 0, 0, 0);
       // one fragment read of k-step 1 after each product of k-step 0, so the
       // reads stream under the products and are in long before their use
       if (ks == 0) {
@@ -359,8 +360,8 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       for (int i = 0; i < TM16; ++i) {  // slab i: product block row i
 #pragma unroll
         for (int j = 0; j < TN16; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) stg[(srow + e) * PWH + j * 16 + scol] = to_f16(acc[i][j][e]);
+          *reinterpret_cast<half4*>(stg + scol * PWH + j * 16 + srow) =
+              half4{to_f16(acc[i][j][0]), to_f16(acc[i][j][1]), to_f16(acc[i][j][2]), to_f16(acc[i][j][3])};
         const int rbase = m0 + wm * WM + i * 16;
         const int cbase = n0 + wn * OW;
 #pragma unroll
@@ -412,8 +413,7 @@ __global__ __launch_bounds__(VM * 128) void gemm_f16_dma(GemmParams p) {
       for (int h = 0; h < 2; ++h)
   #pragma unroll
         for (int j = 0; j < TN16; ++j)
-  #pragma unroll
-          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * PWF + j * 16 + scol] = acc[2 * i + h][j][e];
+          *reinterpret_cast<float4_t*>(stg + (16 * h + scol) * PWF + j * 16 + srow) = acc[2 * i + h][j];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
       if constexpr (EPI != 1) {
@@ -632,7 +632,10 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       FB[fb][q - 8] = *reinterpret_cast<const frag*>(reinterpret_cast<const char*>(sB(sb)) + wn * WN * kBK * 2 +
                                                      goff[ks] + (q - 8) * 16 * kBK * 2);
   };
-  // acc[I][J] holds rows 16 I + 4 (lane / 16) + e, column 16 J + lane % 16
+  // acc[I][J] holds row 16 I + lane % 16, columns 16 J + 4 (lane / 16) + e
+  // (weights as the A operand: the transposed block, so a lane's four
+  // results are consecutive columns of one row and stage as one 8- or
+  // 16-byte LDS write)
   float4_t acc[8][TN16];
 
   const int nk = p.K / kBK;
@@ -690,7 +693,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
 #pragma unroll
       for (int m = 0; m < P; ++m) {
         const int I = m / TN16, J = m % TN16;
-        acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(FA[I], FB[ks][J], acc[I][J], 0, 0, 0);
+        acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(FB[ks][J], FA[I], acc[I][J], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         if (ks == 0) {
           if (J == TN16 - 1) rd(ca, cb, 1, I, 0);
@@ -777,8 +780,8 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
         for (int j = 0; j < TN16; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) stg[(srow + e) * PWH + j * 16 + scol] = to_f16(acc[i][j][e]);
+          *reinterpret_cast<half4*>(stg + scol * PWH + j * 16 + srow) =
+              half4{to_f16(acc[i][j][0]), to_f16(acc[i][j][1]), to_f16(acc[i][j][2]), to_f16(acc[i][j][3])};
         const int rbase = m0 + wm * WM + i * 16;
         const int cbase = n0 + wn * OW;
 #pragma unroll
@@ -848,8 +851,7 @@ __global__ __launch_bounds__(256) void gemm_f16_w4(GemmParams p) {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int j = 0; j < TN16; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) stg[(16 * h + srow + e) * PWF + j * 16 + scol] = acc[2 * i + h][j][e];
+          *reinterpret_cast<float4_t*>(stg + (16 * h + scol) * PWF + j * 16 + srow) = acc[2 * i + h][j];
       const int rbase = m0 + wm * WM + i * 32;
       const int cbase = n0 + wn * OW;
       float4 v[PER], res[PER];
