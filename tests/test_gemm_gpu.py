@@ -64,7 +64,10 @@ def test_gemm_projection_shapes(clef, N, dtype):
 
 @gpu
 @pytest.mark.parametrize("M,N,K", [(2100, 12300, 128), (2100, 12300, 2048), (2048, 9216, 2048), (4096, 12288, 192),
-                                   (2100, 2100, 256)])  # the last: 289 tiles of 128 x 128
+                                   (2100, 2100, 256),  # 289 tiles of 128 x 128
+                                   # 256 x 128 tiles on four waves: one whole round, and
+                                   # ragged rows and columns
+                                   (4096, 2048, 512), (4000, 1900, 320)])
 def test_gemm_persistent_launches(clef, M, N, K):
     """More tiles than CUs: one work-group per CU runs several tiles, the
     next tile's first stages requested during the current one's last.
