@@ -303,7 +303,12 @@ __global__ __launch_bounds__(256) void conv_silu_varlen_kernel(const TI* __restr
         const int tap = k - (4 - taps);
         const int tp = t - 3 + k;
         if (tap >= 0 && avail - (3 - k) >= 0) {
-          const float v = tp >= start ? raw[u + k].at(j) : hist[(int64_t)s * hs + (int64_t)(hrows + tp - start) * W + c0 + j];
+          // own tokens read again from x (L2-resident: the run's rows were
+          // just loaded) rather than from raw[]: this loop stays rolled, and
+          // indexing raw[] in it would put the array in scratch memory for
+          // every run, the unchecked ones included
+          const float v = tp >= start ? static_cast<float>(x[(int64_t)tp * ldx + c0 + j])
+                                      : hist[(int64_t)s * hs + (int64_t)(hrows + tp - start) * W + c0 + j];
           acc = add_rn(acc, mul_rn(v, wt[j][tap]));
         }
       }
