@@ -51,11 +51,12 @@ def parse():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size reference for "
                          "HBM byte counters under rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=("gemm", "gemm_vendor", "attention", "scan"), default=None,
+    ap.add_argument("--only", choices=("gemm", "gemm_vendor", "attention", "scan", "ragged"), default=None,
                     help="run five calls of one kernel workload and exit (for counter profiles): the f16 "
                          "projection GEMM (default 4096 x 12288 x 2048), the same product through "
                          "torch.matmul (the vendor BLAS, for a side-by-side profile), the attention core at "
-                         "T=4096 (16 q / 2 kv heads, d=256), or the full-layer scan (mixed profile)")
+                         "T=4096 (16 q / 2 kv heads, d=256), the full-layer scan (mixed profile), or the "
+                         "ragged prefill (32 requests behind a 512-token prefix, mixed profile)")
     ap.add_argument("--gemm-shape", default="4096,12288,2048",
                     help="M,N,K of --only gemm / gemm_vendor (y[M,N] = x[M,K] . W[N,K]^T, f16 in and out)")
     return ap.parse_args()
@@ -84,6 +85,15 @@ def only_workload(name, torch, gemm_shape="4096,12288,2048"):
         vt = torch.randn((KV, d, T), generator=gen, device=dev).half()
         gate = torch.randn((T, H, d), generator=gen, device=dev).half()
         fn = lambda: clef_hip.attention_gated(q, k, vt, gate)
+    elif name == "ragged":
+        import numpy as np
+        cfg = workloads.block_config()
+        model = clef_hip.Backbone(cfg, workloads.block_weights(cfg, seed=3, device=dev), profile="mixed",
+                                  max_tokens=512 + 4096)
+        prefix_ids, lens, req_ids, cu = workloads.ragged_workload(cfg, seed=4)
+        _, state = model.prefill(np.concatenate([prefix_ids, req_ids[:1]]), capture=512)
+        hidden = torch.empty((int(lens.sum()), cfg["hidden_size"]), dtype=torch.float32, device=dev)
+        fn = lambda: model.prefill_varlen(req_ids, cu, initial=state, hidden=hidden)
     else:
         q, k, v, g, beta = workloads.scan_inputs(2, 4096, 16, 32, 128, 128, dtype=torch.float16, device=dev)
         out = torch.empty((4096, 32, 128), device=dev)
